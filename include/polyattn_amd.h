@@ -1,0 +1,161 @@
+/*
+ * polyattn_amd.h -- C ABI of the MI355X (gfx950) block-sparse masked attention path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (passed as
+ * void*), launches asynchronously on that stream and returns 0 on success or a
+ * negative PA_E* code; pa_last_error() then describes the failure.  Nothing here
+ * allocates device memory: callers own every buffer.
+ *
+ * The reference (polyattn, gpu/ directory) has no native code; the functions below
+ * replace the Python/numpy/Triton functions cited on each declaration.
+ */
+#ifndef POLYATTN_AMD_H
+#define POLYATTN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------ */
+#define PA_OK 0
+#define PA_E_INVALID (-1)     /* argument outside what the kernels support        */
+#define PA_E_HIP (-2)         /* a HIP runtime call failed (message has the code)  */
+#define PA_E_UNSUPPORTED (-3) /* valid request, no kernel variant built for it     */
+
+/* ---- element types ------------------------------------------------------------ */
+#define PA_F32 0
+#define PA_F16 1
+#define PA_BF16 2
+
+/* ---- mask predicate kinds ------------------------------------------------------
+ * 0..5 are the integer kind constants of gpu/masks_gpu.py:9 and
+ * gpu/triton_attn.py:23-27 and keep their values.  d = q - kv in ORIGINAL
+ * coordinates (after perm_q / perm_kv are applied).
+ *   CAUSAL         d >= 0
+ *   WINDOW         0 <= d < p0
+ *   DILATED        d >= 0 and d % p0 == 0
+ *   LOCAL_STRIDED  d >= 0 and (d < p0 or d % p1 == 0)
+ *   TWOBAND        d >= 0 and (d < p0 or p1 <= d < p1 + p2)
+ *   SINKS          d >= 0 and (d < p0 or kv < p1)     (gpu/masks_gpu.py:51-52)
+ *   PREFIX_LM      d >= 0 or (q < p0 and kv < p0)      (src/polyattn/masks.py:129-148)
+ *   FULL           always live
+ *   DENSE          bit (q, kv) of pa_mask.dense_bits
+ */
+#define PA_CAUSAL 0
+#define PA_WINDOW 1
+#define PA_DILATED 2
+#define PA_LOCAL_STRIDED 3
+#define PA_TWOBAND 4
+#define PA_SINKS 5
+#define PA_PREFIX_LM 6
+#define PA_FULL 7
+#define PA_DENSE 8
+
+#define PA_MAX_TERMS 8
+
+typedef struct pa_term {
+  int32_t kind, p0, p1, p2;
+} pa_term;
+
+/* live(q, kv) = (OR over the n_include first terms) AND NOT (OR over the next
+ * n_exclude terms).  A single reference kind is n_include = 1, n_exclude = 0. */
+typedef struct pa_mask {
+  int32_t n_include;
+  int32_t n_exclude;
+  pa_term terms[PA_MAX_TERMS];
+  const int32_t* perm_q;       /* device [N]: index-space row -> original row; NULL = identity */
+  const int32_t* perm_kv;      /* device [N]: index-space col -> original col; NULL = identity */
+  const uint32_t* dense_bits;  /* device, PA_DENSE only: word[q * dense_words + kv / 32] bit kv % 32 */
+  int64_t dense_words;
+} pa_mask;
+
+/* ---- library ------------------------------------------------------------------ */
+const char* pa_last_error(void);   /* message of the last failing call on this thread */
+int32_t pa_abi_version(void);      /* bumped whenever a struct below changes layout   */
+
+/* ---- block index (replaces gpu/blockindex.py:32-51 build) ------------------------
+ * Two phases so the caller can size the padded lists exactly as the reference does
+ * (row pitch = max kv_num, gpu/blockindex.py:42-43).
+ *
+ * pa_index_classify evaluates the predicate on every (q, kv) pair and writes, per
+ * (BQ x A) tile, a code of 2 bits per wave group (32 query rows x min(A, 32) kv
+ * columns; group g = row_group * max(1, A/32) + col_group): bit 2g = some pair live,
+ * bit 2g+1 = every pair live.  A tile is listed iff some group is live; it is FULL
+ * iff every group is full.  kv_num[i] = listed tiles in query block i.
+ * totals[0] = listed tiles, totals[1] = live pairs, totals[2] = max kv_num.
+ * Requires N % BQ == 0, N % A == 0, BQ, A in {16, 32, 64, 128}. */
+int pa_index_classify(const pa_mask* mask, int64_t N, int32_t BQ, int32_t A,
+                      uint32_t* tile_codes /* [N/BQ * N/A] */, int32_t* kv_num /* [N/BQ] */,
+                      unsigned long long* totals /* [3] */, void* stream);
+
+/* Compacts the codes into ascending kv tile lists, zero padded to `pitch` columns:
+ * kv_idx int32 [N/BQ, pitch], kv_partial int8 [N/BQ, pitch] (1 = not full),
+ * kv_wave_bits uint32 [N/BQ, pitch] (the tile code; may be NULL). */
+int pa_index_compact(const uint32_t* tile_codes, const int32_t* kv_num, int64_t N, int32_t BQ,
+                     int32_t A, int32_t* kv_idx, int8_t* kv_partial, uint32_t* kv_wave_bits,
+                     int64_t pitch, void* stream);
+
+/* ---- class-A permutation (replaces gpu/permute.py:12-31) -------------------------
+ * Row gather dst[b, p, :] = src[b, perm[p], :] (inverse = 0), the index_select of
+ * gpu/permute.py:22-24, or row scatter dst[b, perm[p], :] = src[b, p, :] (inverse = 1),
+ * the un-permute of gpu/test_correctness.py:77.  Strides are in bytes; row_bytes is
+ * the contiguous length of one row. */
+int pa_permute_rows(const void* src, void* dst, const int32_t* perm, int64_t BH, int64_t N,
+                    int64_t row_bytes, int64_t src_bh_stride, int64_t src_row_stride,
+                    int64_t dst_bh_stride, int64_t dst_row_stride, int32_t inverse, void* stream);
+
+/* inv[perm[p]] = p  (gpu/permute.py:27-31). */
+int pa_invert_perm(const int32_t* perm, int32_t* inv, int64_t N, void* stream);
+
+/* perm[p] = original position at permuted position p for the residue-class sort
+ * by (i mod s, i div s) (gpu/permute.py:12-15), any N >= 1, s >= 1. */
+int pa_residue_perm(int32_t* perm, int64_t N, int32_t s, void* stream);
+
+/* ---- attention forward (replaces gpu/triton_attn.py:62-241) ----------------------- */
+typedef struct pa_attn_args {
+  const void* q;  /* [BH, N, D] rows of D contiguous elements */
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t q_sb, q_sn, k_sb, k_sn, v_sb, v_sn, o_sb, o_sn; /* strides in elements */
+  int64_t BH, N;
+  int32_t D;      /* 64 or 128 */
+  int32_t dtype;  /* PA_F32 / PA_F16 / PA_BF16 for q, k, v and o */
+  float scale;    /* softmax scale, usually D ** -0.5 */
+  int32_t BQ, A;  /* tile shape of the block index */
+  const int32_t* kv_idx;        /* [N/BQ, pitch] */
+  const int32_t* kv_num;        /* [N/BQ] */
+  const int8_t* kv_partial;     /* [N/BQ, pitch] */
+  const uint32_t* kv_wave_bits; /* [N/BQ, pitch] or NULL: per-wave skip and mask bits */
+  int64_t pitch;
+  pa_mask mask;   /* predicate applied on partial tiles, in original coordinates */
+  int32_t gather_q;   /* load query rows through mask.perm_q (Q not physically permuted) */
+  int32_t gather_kv;  /* load key/value rows through mask.perm_kv (gpu/triton_attn.py:104-107) */
+  int32_t scatter_o;  /* store output row r at mask.perm_q[r] (fused inverse permutation) */
+  float* lse;         /* NULL or [BH, N] fp32, natural-log sum-exp of the stored rows */
+  int64_t lse_sb;
+  const void* prev_o;      /* NULL or a partial result over a disjoint sub-mask, same
+                              row order as o; merged by log-sum-exp into o */
+  int32_t prev_dtype;      /* PA_F32 / PA_F16 / PA_BF16 */
+  int64_t prev_sb, prev_sn;
+  const float* prev_lse;   /* [BH, N] stride lse_sb, required with prev_o */
+  const int32_t* qblock_order; /* NULL or [N/BQ] permutation: order query blocks are issued */
+} pa_attn_args;
+
+int pa_attn_fwd(const pa_attn_args* args, void* stream);
+
+/* ---- log-sum-exp merge of a disjoint split (spec: src/polyattn/experiments/compose.py:7-17)
+ * o[b, r, :] = sum_k exp(lse_k - M) o_k / sum_k exp(lse_k - M), M = max_k lse_k;
+ * rows with every lse_k = -inf give 0 and lse -inf.  parts are fp32 [BH, N, D]
+ * contiguous; o is dtype `out_dtype` contiguous; lse_out may be NULL. */
+int pa_lse_merge(const float* const* o_parts, const float* const* lse_parts, int32_t n_parts,
+                 void* o, int32_t out_dtype, float* lse_out, int64_t BH, int64_t N, int32_t D,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POLYATTN_AMD_H */

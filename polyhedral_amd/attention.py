@@ -1,0 +1,151 @@
+"""Block-sparse masked attention forward: the call surface of gpu/triton_attn.py on HIP.
+
+block_sparse_attention keeps the reference signature (gpu/triton_attn.py:185-189),
+its defaults, asserts and return value, and runs pa_attn_fwd (a hand-written
+gfx950 kernel) instead of the Triton JIT.  Differences a caller can observe:
+
+* SINKS partial tiles apply the sink term on absolute kv (kv < p1), as the ground
+  truth gpu/masks_gpu.py:51-52 and gpu/reference.py do; the reference's _live
+  drops it (gpu/triton_attn.py:56-59).
+* ``kind`` may also be a spec.MaskSpec (unions and set differences of kinds) or a
+  spec.DeviceMask (any predicate blockindex.build accepts, explicit matrices
+  included), and kind PREFIX_LM = 6 exists.
+* num_warps / num_stages are Triton launch knobs; every (num_warps, num_stages) of
+  gpu/launchsweep.py:15-16 is accepted and the HIP kernel's shape is fixed by
+  (BQ, A, D, dtype), so there is no pipeliner fallback to take.
+* gather_mult > 1 (the class-B traffic emulation of gpu/triton_attn.py:109-128)
+  raises NotImplementedError.
+
+Keyword-only extensions: kv_wave_bits (per-wave skip codes; found automatically for
+an index made by blockindex.build / to_cuda), gather_q / scatter_o (read Q rows
+through perm_q and write O rows back to original positions: the class-A
+permutation fused into the kernel's loads and stores), lse (write the natural-log
+sum-exp per row), prev = (o_prev, lse_prev) (merge a partial over a disjoint
+sub-mask by log-sum-exp in the epilogue), out, qblock_order.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from .index import wave_bits_for
+from .spec import DeviceMask, MaskSpec, as_perm_tensor
+
+CAUSAL, WINDOW, DILATED, LOCAL_STRIDED, TWOBAND, SINKS, PREFIX_LM = 0, 1, 2, 3, 4, 5, 6
+
+_PIPELINE_FALLBACK = set()
+
+
+def _assert_kinds_match():
+    """The kind constants here and in masks_gpu must agree (gpu/triton_attn.py:32-38)."""
+    from . import registry as _m
+    mine = dict(CAUSAL=CAUSAL, WINDOW=WINDOW, DILATED=DILATED, LOCAL_STRIDED=LOCAL_STRIDED,
+                TWOBAND=TWOBAND, SINKS=SINKS, PREFIX_LM=PREFIX_LM)
+    theirs = {k: getattr(_m, k) for k in mine}
+    if mine != theirs:
+        raise RuntimeError(f"kind constants diverged: triton_attn={mine} masks_gpu={theirs}")
+
+
+def _rows3(t, name):
+    if t.dim() != 3:
+        raise ValueError(f"{name} must be [BH, N, D]")
+    if t.stride(2) != 1:
+        raise ValueError(f"{name} needs a unit-stride last dimension")
+    return t
+
+
+def block_sparse_attention(q, k, v, kv_idx, kv_num, kv_partial,
+                           kind, p0, p1, p2, BQ, A, scale=None,
+                           perm_q=None, perm_kv=None, gather_kv=False,
+                           gather_mult=1, gather_scatter=True,
+                           num_warps=4, num_stages=2, *,
+                           kv_wave_bits=None, gather_q=False, scatter_o=False,
+                           lse=None, prev=None, out=None, qblock_order=None):
+    """q, k, v: [BH, N, D] (float32 / float16 / bfloat16). Returns o [BH, N, D], dtype of q.
+
+    perm_q / perm_kv: int32 [N], permuted position -> ORIGINAL position, used to
+    evaluate the mask in original coordinates (identity when None)."""
+    BH, N, D = q.shape
+    if perm_kv is None:
+        perm_kv = perm_q
+    _assert_kinds_match()
+    assert N % BQ == 0 and N % A == 0, "cost model and kernel both assume this"
+    assert k.shape == v.shape == q.shape
+    if gather_mult != 1:
+        raise NotImplementedError("gather_mult > 1 (class-B traffic emulation) is not built")
+    _lib.require_device(q, k, v, kv_idx, kv_num, kv_partial)
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _rows3(t, n)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k, v must share a dtype")
+    kv_idx = kv_idx.contiguous()
+    kv_num = kv_num.contiguous()
+    kv_partial = kv_partial.contiguous()
+    nq = N // BQ
+    if kv_num.numel() != nq or kv_idx.dim() != 2 or kv_idx.shape[0] != nq or kv_partial.shape != kv_idx.shape:
+        raise ValueError(f"block index shapes {tuple(kv_idx.shape)} / {tuple(kv_num.shape)} / "
+                         f"{tuple(kv_partial.shape)} do not match N/BQ = {nq}")
+    if kv_idx.dtype != torch.int32 or kv_num.dtype != torch.int32 or kv_partial.dtype != torch.int8:
+        raise TypeError("block index must be int32 / int32 / int8")
+    if kv_wave_bits is None:
+        kv_wave_bits = wave_bits_for(kv_idx, BQ, A)
+    if kv_wave_bits is not None:
+        kv_wave_bits = kv_wave_bits.to(torch.int32).contiguous()
+        if kv_wave_bits.shape != kv_idx.shape:
+            raise ValueError("kv_wave_bits must have the shape of kv_idx")
+
+    dev = q.device
+    if isinstance(kind, DeviceMask):
+        if perm_q is not None:
+            raise ValueError("a DeviceMask carries its own permutation; pass no perm_q / perm_kv")
+        dmask = kind
+    else:
+        dmask = DeviceMask(MaskSpec.of(kind, p0, p1, p2), as_perm_tensor(perm_q, dev),
+                           as_perm_tensor(perm_kv, dev))
+    o = out if out is not None else torch.empty_like(q)
+    _rows3(o, "out")
+    if o.shape != q.shape or o.dtype != q.dtype:
+        raise ValueError("out must match q in shape and dtype")
+
+    args = _lib.PaAttnArgs()
+    args.q, args.k, args.v, args.o = _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o)
+    args.q_sb, args.q_sn = q.stride(0), q.stride(1)
+    args.k_sb, args.k_sn = k.stride(0), k.stride(1)
+    args.v_sb, args.v_sn = v.stride(0), v.stride(1)
+    args.o_sb, args.o_sn = o.stride(0), o.stride(1)
+    args.BH, args.N, args.D = BH, N, D
+    args.dtype = _lib.dtype_code(q)
+    args.scale = float(scale or D ** -0.5)
+    args.BQ, args.A = BQ, A
+    args.kv_idx, args.kv_num, args.kv_partial = _lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial)
+    args.kv_wave_bits = _lib.ptr(kv_wave_bits)
+    args.pitch = kv_idx.shape[1]
+    args.mask = dmask.struct()
+    args.gather_q, args.gather_kv, args.scatter_o = int(bool(gather_q)), int(bool(gather_kv)), int(bool(scatter_o))
+    if lse is not None:
+        _lib.require_device(lse)
+        if lse.dtype != torch.float32 or lse.shape != (BH, N) or lse.stride(1) != 1:
+            raise ValueError("lse must be float32 [BH, N] with unit row stride")
+        args.lse, args.lse_sb = _lib.ptr(lse), lse.stride(0)
+    if prev is not None:
+        o_prev, lse_prev = prev
+        _lib.require_device(o_prev, lse_prev)
+        _rows3(o_prev, "prev o")
+        if o_prev.shape != q.shape or lse_prev.shape != (BH, N) or lse_prev.dtype != torch.float32:
+            raise ValueError("prev must be (o [BH, N, D], lse float32 [BH, N])")
+        if lse is not None and lse.stride(0) != lse_prev.stride(0):
+            raise ValueError("lse and prev lse must share their row stride")
+        if lse_prev.stride(1) != 1:
+            raise ValueError("prev lse needs a unit row stride")
+        args.prev_o, args.prev_dtype = _lib.ptr(o_prev), _lib.dtype_code(o_prev)
+        args.prev_sb, args.prev_sn = o_prev.stride(0), o_prev.stride(1)
+        args.prev_lse = _lib.ptr(lse_prev)
+        args.lse_sb = lse_prev.stride(0)
+    if qblock_order is not None:
+        qblock_order = qblock_order.to(device=dev, dtype=torch.int32).contiguous()
+        if qblock_order.numel() != nq:
+            raise ValueError("qblock_order must have N/BQ entries")
+        args.qblock_order = _lib.ptr(qblock_order)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().pa_attn_fwd(ctypes.byref(args), _lib.stream_of(q)), "pa_attn_fwd")
+    return o

@@ -1,0 +1,79 @@
+"""Compile the HIP sources into polyhedral_amd/_lib/libpolyattn_amd.so (gfx950).
+
+The library links against the HIP runtime bundled with PyTorch (torch/lib), whose
+soname (libamdhip64.so.7) is the one already loaded by ``import torch``, so one
+process never holds two HIP runtimes.  Objects are built in parallel into
+polyhedral_amd/_build/ and linked in place; every call recompiles.
+"""
+import concurrent.futures as cf
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+PKG = pathlib.Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIBDIR = PKG / "_lib"
+LIB = LIBDIR / "libpolyattn_amd.so"
+ARCH = "gfx950"
+
+SOURCES = ["common.hip", "index.hip", "permute.hip", "merge.hip", "attn_fwd.hip",
+           "attn_bf16.hip", "attn_f16.hip", "attn_f32.hip"]
+
+# -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object-version=5",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             f"-I{ROOT / 'include'}", f"-I{CSRC}"]
+
+
+def _hipcc():
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
+
+
+def _torch_lib():
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.origin:
+        raise RuntimeError("torch is not importable; its HIP runtime is what the library links to")
+    return pathlib.Path(spec.origin).parent / "lib"
+
+
+def _compile(src, hipcc):
+    obj = BUILD / (pathlib.Path(src).stem + ".o")
+    cmd = [hipcc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in r.stderr.splitlines() if "not a recognized feature" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{err}")
+    return obj
+
+
+def build(verbose=False, jobs=None):
+    """Compile every source and link the shared library.  Returns its path."""
+    hipcc = _hipcc()
+    BUILD.mkdir(exist_ok=True)
+    LIBDIR.mkdir(exist_ok=True)
+    jobs = jobs or min(len(SOURCES), max(1, os.cpu_count() or 1))
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, hipcc), SOURCES))
+    tl = _torch_lib()
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc, "-shared", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs),
+           f"-L{tl}", "-lamdhip64", f"-Wl,-rpath,{tl}", "-Wl,-soname,libpolyattn_amd.so"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}", file=sys.stderr)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)

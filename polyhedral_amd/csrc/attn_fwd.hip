@@ -1,0 +1,88 @@
+// C-ABI entry of the attention forward: argument checks, then dispatch to the
+// (dtype, D, waves) instantiation.  Mirrors the checks of the reference entry
+// point gpu/triton_attn.py:185-241 (N % BQ, N % A, shapes) and reports them as
+// PA_E_INVALID with a message instead of an AssertionError.
+#include "attn_kernel.hpp"
+
+namespace pa {
+int launch_attn_bf16(const AttnK& a, int D, int NW, hipStream_t s);
+int launch_attn_f16(const AttnK& a, int D, int NW, hipStream_t s);
+int launch_attn_f32(const AttnK& a, int D, int NW, hipStream_t s);
+}  // namespace pa
+
+extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
+  PA_CHECK_ARG(x != nullptr, "pa_attn_fwd: null args");
+  PA_CHECK_ARG(x->q && x->k && x->v && x->o, "pa_attn_fwd: null q/k/v/o");
+  PA_CHECK_ARG(x->kv_idx && x->kv_num && x->kv_partial, "pa_attn_fwd: null block index");
+  PA_CHECK_ARG(x->D == 64 || x->D == 128, "pa_attn_fwd: D=%d (supported: 64, 128)", x->D);
+  PA_CHECK_ARG(x->dtype == PA_F32 || x->dtype == PA_F16 || x->dtype == PA_BF16, "pa_attn_fwd: dtype %d",
+               x->dtype);
+  PA_CHECK_ARG(x->BH >= 1 && x->N >= 1 && x->N <= (1ll << 30), "pa_attn_fwd: BH=%lld N=%lld",
+               (long long)x->BH, (long long)x->N);
+  const bool tile_ok = (x->BQ == 16 || x->BQ == 32 || x->BQ == 64 || x->BQ == 128) &&
+                       (x->A == 16 || x->A == 32 || x->A == 64 || x->A == 128);
+  PA_CHECK_ARG(tile_ok, "pa_attn_fwd: tile %dx%d (BQ, A each in 16, 32, 64, 128)", x->BQ, x->A);
+  PA_CHECK_ARG(x->N % x->BQ == 0 && x->N % x->A == 0, "pa_attn_fwd: N=%lld not divisible by BQ=%d, A=%d",
+               (long long)x->N, x->BQ, x->A);
+  PA_CHECK_ARG(x->pitch >= 0, "pa_attn_fwd: negative pitch");
+  PA_CHECK_ARG(!(x->gather_q || x->scatter_o) || x->mask.perm_q,
+               "pa_attn_fwd: gather_q / scatter_o need mask.perm_q");
+  PA_CHECK_ARG(!x->gather_kv || x->mask.perm_kv, "pa_attn_fwd: gather_kv needs mask.perm_kv");
+  PA_CHECK_ARG(!x->prev_o || x->prev_lse, "pa_attn_fwd: prev_o needs prev_lse");
+  PA_CHECK_ARG(!x->prev_o || x->prev_dtype == PA_F32 || x->prev_dtype == PA_F16 || x->prev_dtype == PA_BF16,
+               "pa_attn_fwd: prev_dtype %d", x->prev_dtype);
+  PA_CHECK_ARG(!x->prev_o || x->lse_sb >= x->N, "pa_attn_fwd: lse_sb=%lld < N", (long long)x->lse_sb);
+  PA_CHECK_ARG(!x->lse || x->lse_sb >= x->N, "pa_attn_fwd: lse_sb=%lld < N", (long long)x->lse_sb);
+  if (int rc = pa::check_mask(&x->mask, x->N)) return rc;
+  // 16-B vector access of every row start
+  const int esz = x->dtype == PA_F32 ? 4 : 2;
+  auto al = [&](const void* p, int64_t sb, int64_t sn) {
+    return (reinterpret_cast<uintptr_t>(p) % 16) == 0 && (sb * esz) % 16 == 0 && (sn * esz) % 16 == 0;
+  };
+  PA_CHECK_ARG(al(x->q, x->q_sb, x->q_sn) && al(x->k, x->k_sb, x->k_sn) && al(x->v, x->v_sb, x->v_sn) &&
+                   al(x->o, x->o_sb, x->o_sn),
+               "pa_attn_fwd: q/k/v/o rows must be 16-byte aligned");
+
+  pa::AttnK a;
+  a.q = static_cast<const char*>(x->q);
+  a.k = static_cast<const char*>(x->k);
+  a.v = static_cast<const char*>(x->v);
+  a.o = static_cast<char*>(x->o);
+  a.q_sb = x->q_sb; a.q_sn = x->q_sn;
+  a.k_sb = x->k_sb; a.k_sn = x->k_sn;
+  a.v_sb = x->v_sb; a.v_sn = x->v_sn;
+  a.o_sb = x->o_sb; a.o_sn = x->o_sn;
+  a.N = (int32_t)x->N;
+  a.BQ = x->BQ;
+  a.A = x->A;
+  a.nq = (int32_t)(x->N / x->BQ);
+  a.total_wg = (int64_t)a.nq * x->BH;
+  a.c = x->scale * 1.4426950408889634f;
+  a.kv_idx = x->kv_idx;
+  a.kv_num = x->kv_num;
+  a.kv_partial = x->kv_partial;
+  a.kv_wave_bits = x->kv_wave_bits;
+  a.pitch = x->pitch;
+  a.pred = pa::make_pred(x->mask);
+  a.gather_q = x->gather_q;
+  a.gather_kv = x->gather_kv;
+  a.scatter_o = x->scatter_o;
+  a.lse = x->lse;
+  a.lse_sb = x->lse_sb;
+  a.prev_o = static_cast<const char*>(x->prev_o);
+  a.prev_dtype = x->prev_dtype;
+  a.prev_sb = x->prev_sb;
+  a.prev_sn = x->prev_sn;
+  a.prev_lse = x->prev_lse;
+  a.qblock_order = x->qblock_order;
+  PA_CHECK_ARG(a.total_wg <= 0x7fffffffll, "pa_attn_fwd: %lld work-groups exceed the grid limit",
+               (long long)a.total_wg);
+
+  const int NW = x->BQ >= 32 ? x->BQ / 32 : 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (x->dtype) {
+    case PA_BF16: return pa::launch_attn_bf16(a, x->D, NW, s);
+    case PA_F16: return pa::launch_attn_f16(a, x->D, NW, s);
+    default: return pa::launch_attn_f32(a, x->D, NW, s);
+  }
+}

@@ -1,0 +1,212 @@
+// Block-index builder on the GPU: mask predicate -> per-query-block lists of live
+// KV tiles.  Replaces gpu/blockindex.py:32-51 (build), which materialises the N x N
+// mask on the host and tiles it with numpy any/all.
+//
+// Phase 1 (classify): one work-group per query block walks every KV column in
+// chunks of 256, evaluates the predicate for the block's BQ rows and folds the
+// result into per-tile codes: 2 bits (some live / all live) per wave group of
+// 32 query rows x min(A, 32) columns.  Wave ballots do the column reduction.
+// Phase 2 (compact): one work-group per query block scans the tile codes and
+// writes the ascending, zero-padded kv_idx / kv_partial / kv_wave_bits rows.
+#include "common.hpp"
+
+namespace pa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 256;  // columns per pass, one per thread
+
+__global__ void zero_totals_kernel(unsigned long long* totals) {
+  if (threadIdx.x < 3) totals[threadIdx.x] = 0ull;
+}
+
+__global__ __launch_bounds__(kThreads) void classify_kernel(const Pred pred, int32_t N, int32_t BQ,
+                                                             int32_t A, uint32_t* __restrict__ codes,
+                                                             int32_t* __restrict__ kv_num,
+                                                             unsigned long long* __restrict__ totals) {
+  __shared__ int32_t q_orig[128];
+  __shared__ uint32_t tile_code[kChunk / 16];
+  __shared__ int32_t red_live[kThreads / 64];
+  __shared__ int32_t red_tiles;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int qb = blockIdx.x;
+  const int nk = N / A;
+  const int rg_rows = BQ < 32 ? BQ : 32;   // rows per wave group
+  const int n_rg = BQ / rg_rows;
+  const int cw = A < 32 ? A : 32;          // columns per wave group
+  const int ncg = A / cw;
+
+  if (tid < BQ) {
+    const int r = qb * BQ + tid;
+    q_orig[tid] = pred.perm_q ? pred.perm_q[r] : r;
+  }
+  if (tid == 0) red_tiles = 0;
+  __syncthreads();
+
+  int32_t live_count = 0;
+  int32_t tiles_listed = 0;  // meaningful in thread 0 only
+
+  for (int c0 = 0; c0 < N; c0 += kChunk) {
+    if (tid < kChunk / 16) tile_code[tid] = 0u;
+    __syncthreads();
+
+    const int col = c0 + tid;
+    const bool valid = col < N;
+    uint32_t any_rg = 0u, all_rg = 0u;
+    if (valid) {
+      const int32_t ko = pred.perm_kv ? pred.perm_kv[col] : col;
+      for (int g = 0; g < n_rg; ++g) {
+        bool any = false, all = true;
+        for (int rr = 0; rr < rg_rows; ++rr) {
+          const bool live = pred_live(pred, q_orig[g * rg_rows + rr], ko);
+          any |= live;
+          all &= live;
+          live_count += live ? 1 : 0;
+        }
+        any_rg |= (any ? 1u : 0u) << g;
+        all_rg |= (all ? 1u : 0u) << g;
+      }
+    }
+    // Column reduction inside each wave: a column group never straddles a wave.
+    const int wave_col0 = c0 + wave * 64;
+    for (int g = 0; g < n_rg; ++g) {
+      const unsigned long long b_any = __ballot((any_rg >> g) & 1u);
+      const unsigned long long b_all = __ballot((all_rg >> g) & 1u);
+      const int ngroups_in_wave = 64 / cw;
+      if (lane < ngroups_in_wave) {
+        const int gc0 = wave_col0 + lane * cw;  // first column of this column group
+        if (gc0 < N) {
+          const unsigned long long gm = (cw == 64 ? ~0ull : ((1ull << cw) - 1ull)) << (lane * cw);
+          const bool gany = (b_any & gm) != 0ull;
+          const bool gall = (b_all & gm) == gm;
+          const int cg = (gc0 % A) / cw;
+          const int code_g = g * ncg + cg;
+          const uint32_t bits = (gany ? 1u : 0u) << (2 * code_g) | (gall ? 1u : 0u) << (2 * code_g + 1);
+          if (bits) atomicOr(&tile_code[(gc0 - c0) / A], bits);
+        }
+      }
+    }
+    __syncthreads();
+    const int tiles_in_chunk = kChunk / A;
+    if (tid < tiles_in_chunk) {
+      const int kb = c0 / A + tid;
+      if (kb < nk) {
+        const uint32_t code = tile_code[tid];
+        codes[(int64_t)qb * nk + kb] = code;
+        if (code & 0x55555555u) atomicAdd(&red_tiles, 1);
+      }
+    }
+    __syncthreads();
+  }
+
+  // live pairs: wave reduce, then one atomic per work-group
+  for (int off = 32; off > 0; off >>= 1) live_count += __shfl_down(live_count, off, 64);
+  if (lane == 0) red_live[wave] = live_count;
+  __syncthreads();
+  if (tid == 0) {
+    long long tot = 0;
+    for (int i = 0; i < kThreads / 64; ++i) tot += red_live[i];
+    tiles_listed = red_tiles;
+    kv_num[qb] = tiles_listed;
+    atomicAdd(&totals[0], (unsigned long long)tiles_listed);
+    atomicAdd(&totals[1], (unsigned long long)tot);
+    atomicMax(&totals[2], (unsigned long long)tiles_listed);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void compact_kernel(const uint32_t* __restrict__ codes,
+                                                            const int32_t* __restrict__ kv_num,
+                                                            int32_t N, int32_t BQ, int32_t A,
+                                                            uint32_t full_mask,
+                                                            int32_t* __restrict__ kv_idx,
+                                                            int8_t* __restrict__ kv_partial,
+                                                            uint32_t* __restrict__ kv_wave_bits,
+                                                            int64_t pitch) {
+  __shared__ int32_t wave_tot[kThreads / 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int qb = blockIdx.x;
+  const int nk = N / A;
+  const int64_t row = (int64_t)qb * pitch;
+  int base = 0;
+  for (int k0 = 0; k0 < nk; k0 += kThreads) {
+    const int kb = k0 + tid;
+    const uint32_t code = kb < nk ? codes[(int64_t)qb * nk + kb] : 0u;
+    const bool listed = (code & 0x55555555u) != 0u;
+    const unsigned long long bal = __ballot(listed);
+    const int before_in_wave = __popcll(bal & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_tot[wave] = __popcll(bal);
+    __syncthreads();
+    int before = base + before_in_wave;
+    int chunk_total = 0;
+    for (int i = 0; i < kThreads / 64; ++i) {
+      if (i < wave) before += wave_tot[i];
+      chunk_total += wave_tot[i];
+    }
+    if (listed && before < pitch) {  // pitch >= kv_num is the caller's contract; never write past it
+      kv_idx[row + before] = kb;
+      kv_partial[row + before] = ((code & full_mask) == full_mask) ? 0 : 1;
+      if (kv_wave_bits) kv_wave_bits[row + before] = code;
+    }
+    base += chunk_total;
+    __syncthreads();
+  }
+  // zero padding up to the pitch (gpu/blockindex.py:44-45 allocates with np.zeros)
+  const int n = kv_num[qb];
+  for (int64_t j = n + tid; j < pitch; j += kThreads) {
+    kv_idx[row + j] = 0;
+    kv_partial[row + j] = 0;
+    if (kv_wave_bits) kv_wave_bits[row + j] = 0u;
+  }
+}
+
+bool tile_ok(int32_t x) { return x == 16 || x == 32 || x == 64 || x == 128; }
+
+}  // namespace
+}  // namespace pa
+
+extern "C" int pa_index_classify(const pa_mask* mask, int64_t N, int32_t BQ, int32_t A,
+                                 uint32_t* tile_codes, int32_t* kv_num, unsigned long long* totals,
+                                 void* stream) {
+  PA_CHECK_ARG(mask != nullptr && tile_codes && kv_num && totals, "pa_index_classify: null argument");
+  PA_CHECK_ARG(N >= 1 && N <= (1ll << 30), "pa_index_classify: N=%lld out of range", (long long)N);
+  PA_CHECK_ARG(pa::tile_ok(BQ) && pa::tile_ok(A),
+               "pa_index_classify: BQ=%d A=%d must each be one of 16, 32, 64, 128", BQ, A);
+  PA_CHECK_ARG(N % BQ == 0 && N % A == 0, "pa_index_classify: N=%lld not divisible by BQ=%d and A=%d",
+               (long long)N, BQ, A);
+  if (int rc = pa::check_mask(mask, N)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const pa::Pred pred = pa::make_pred(*mask);
+  hipLaunchKernelGGL(pa::zero_totals_kernel, dim3(1), dim3(64), 0, s, totals);
+  PA_LAUNCH_CHECK("zero_totals_kernel");
+  hipLaunchKernelGGL(pa::classify_kernel, dim3((unsigned)(N / BQ)), dim3(pa::kThreads), 0, s, pred,
+                     (int32_t)N, BQ, A, tile_codes, kv_num, totals);
+  PA_LAUNCH_CHECK("classify_kernel");
+  return PA_OK;
+}
+
+extern "C" int pa_index_compact(const uint32_t* tile_codes, const int32_t* kv_num, int64_t N, int32_t BQ,
+                                int32_t A, int32_t* kv_idx, int8_t* kv_partial, uint32_t* kv_wave_bits,
+                                int64_t pitch, void* stream) {
+  PA_CHECK_ARG(tile_codes && kv_num, "pa_index_compact: null argument");
+  PA_CHECK_ARG(N >= 1 && N <= (1ll << 30), "pa_index_compact: N=%lld out of range", (long long)N);
+  PA_CHECK_ARG(pa::tile_ok(BQ) && pa::tile_ok(A) && N % BQ == 0 && N % A == 0,
+               "pa_index_compact: bad tile shape BQ=%d A=%d for N=%lld", BQ, A, (long long)N);
+  PA_CHECK_ARG(pitch >= 0, "pa_index_compact: negative pitch");
+  if (pitch == 0) return PA_OK;  // every query block is empty: nothing to write
+  PA_CHECK_ARG(kv_idx && kv_partial, "pa_index_compact: null output");
+  const int rg_rows = BQ < 32 ? BQ : 32;
+  const int cw = A < 32 ? A : 32;
+  const int ngroups = (BQ / rg_rows) * (A / cw);
+  uint32_t full_mask = 0u;
+  for (int g = 0; g < ngroups; ++g) full_mask |= 2u << (2 * g);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(pa::compact_kernel, dim3((unsigned)(N / BQ)), dim3(pa::kThreads), 0, s, tile_codes,
+                     kv_num, (int32_t)N, BQ, A, full_mask, kv_idx, kv_partial, kv_wave_bits, pitch);
+  PA_LAUNCH_CHECK("compact_kernel");
+  return PA_OK;
+}

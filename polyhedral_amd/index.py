@@ -1,0 +1,132 @@
+"""GPU block-index builder: the call surface of gpu/blockindex.py (BlockIndex, build, to_cuda).
+
+build(mask, N, BQ, A) gives the same BlockIndex as gpu/blockindex.py:32-51 --
+ascending live KV tiles per query block, zero padded to max_kv columns, int32 /
+int32 / int8, elements = listed tiles * BQ * A, live = live pairs -- but the
+predicate is evaluated and tiled on the GPU (pa_index_classify / pa_index_compact)
+instead of materialising the N x N mask on the host.  The device arrays stay
+cached on the BlockIndex, so to_cuda hands them out without a second upload; the
+numpy fields are filled from one device-to-host copy to keep the reference's
+dataclass contract.
+
+Extensions (keyword-only): ``perm`` / ``perm_kv`` build the index of a class-A
+relabelled mask without materialising M[perm][:, perm]; ``kv_wave_bits`` is the
+per-tile code of 2 bits per 32-row x 32-column wave group (some live / all live),
+which the attention kernel uses to skip or mask at wave granularity.
+"""
+import ctypes
+import weakref
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from .spec import device_mask
+
+# id(kv_idx device tensor) -> (weakref to it, kv_wave_bits tensor, BQ, A), so the
+# reference call surface (which passes only kv_idx / kv_num / kv_partial) still gets
+# per-wave skipping.  Keyed by id because tensors compare elementwise.
+_WAVE_BITS = {}
+
+
+def _register_wave_bits(kv_idx, wave, BQ, A):
+    key = id(kv_idx)
+    _WAVE_BITS[key] = (weakref.ref(kv_idx), wave, BQ, A)
+    weakref.finalize(kv_idx, _WAVE_BITS.pop, key, None)
+
+
+@dataclass
+class BlockIndex:
+    BQ: int
+    A: int
+    N: int
+    kv_idx: np.ndarray       # [n_q_blocks, max_kv] int32: kv tile ids, ascending
+    kv_num: np.ndarray       # [n_q_blocks] int32
+    kv_partial: np.ndarray   # [n_q_blocks, max_kv] int8: 1 if the mask must be applied
+    elements: int            # listed tiles * BQ * A
+    live: int                # live (q, kv) pairs
+    kv_wave_bits: Optional[np.ndarray] = None  # [n_q_blocks, max_kv] uint32 wave-group codes
+    _device: Optional[tuple] = field(default=None, repr=False, compare=False)
+
+    @property
+    def waste(self):
+        return self.elements / self.live
+
+    @property
+    def tiles(self):
+        return self.elements // (self.BQ * self.A)
+
+    @property
+    def max_kv(self):
+        return int(self.kv_idx.shape[1])
+
+
+def _default_device(device):
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else None
+    if device is None or torch.device(device).type != "cuda":
+        raise RuntimeError("blockindex.build runs on the GPU only (no host builder in the product path)")
+    return torch.device(device)
+
+
+def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None):
+    """Build on the GPU; returns (kv_idx, kv_num, kv_partial, kv_wave_bits, tiles, live) with
+    device tensors and host ints.  One synchronisation (to size the padded lists)."""
+    assert N % BQ == 0 and N % A == 0
+    dev = _default_device(device)
+    dm = device_mask(mask, N, dev, perm=perm, perm_kv=perm_kv)
+    nq, nk = N // BQ, N // A
+    codes = torch.empty(nq * nk, dtype=torch.int32, device=dev)
+    kv_num = torch.empty(nq, dtype=torch.int32, device=dev)
+    totals = torch.empty(3, dtype=torch.int64, device=dev)
+    L = _lib.lib()
+    ms = dm.struct()
+    with torch.cuda.device(dev):
+        stream = _lib.stream_of(codes)
+        _lib.check(L.pa_index_classify(ctypes.byref(ms), N, BQ, A, _lib.ptr(codes), _lib.ptr(kv_num), _lib.ptr(totals),
+                                       stream), "pa_index_classify")
+        tiles, live, max_kv = (int(x) for x in totals.cpu())
+        kv_idx = torch.empty((nq, max_kv), dtype=torch.int32, device=dev)
+        kv_partial = torch.empty((nq, max_kv), dtype=torch.int8, device=dev)
+        wave = torch.empty((nq, max_kv), dtype=torch.int32, device=dev)
+        _lib.check(L.pa_index_compact(_lib.ptr(codes), _lib.ptr(kv_num), N, BQ, A, _lib.ptr(kv_idx),
+                                      _lib.ptr(kv_partial), _lib.ptr(wave), max_kv, stream),
+                   "pa_index_compact")
+    _register_wave_bits(kv_idx, wave, BQ, A)
+    return kv_idx, kv_num, kv_partial, wave, tiles, live
+
+
+def build(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None):
+    """gpu/blockindex.py:32 build(mask, N, BQ, A), computed on the GPU."""
+    kv_idx, kv_num, kv_partial, wave, tiles, live = build_device(mask, N, BQ, A, perm=perm,
+                                                                 perm_kv=perm_kv, device=device)
+    return BlockIndex(BQ, A, N, kv_idx.cpu().numpy(), kv_num.cpu().numpy(), kv_partial.cpu().numpy(),
+                      tiles * BQ * A, live, wave.cpu().numpy().view(np.uint32),
+                      _device=(kv_idx, kv_num, kv_partial, wave))
+
+
+def to_cuda(bi, device="cuda"):
+    """gpu/blockindex.py:54-58: (kv_idx, kv_num, kv_partial) on the device."""
+    dev = torch.device(device)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    if bi._device is not None and bi._device[0].device == dev:
+        return bi._device[:3]
+    kv_idx = torch.from_numpy(np.ascontiguousarray(bi.kv_idx)).to(dev)
+    out = (kv_idx, torch.from_numpy(np.ascontiguousarray(bi.kv_num)).to(dev),
+           torch.from_numpy(np.ascontiguousarray(bi.kv_partial)).to(dev))
+    if bi.kv_wave_bits is not None and dev.type == "cuda":
+        wave = torch.from_numpy(np.ascontiguousarray(bi.kv_wave_bits).view(np.int32)).to(dev)
+        _register_wave_bits(kv_idx, wave, bi.BQ, bi.A)
+    return out
+
+
+def wave_bits_for(kv_idx, BQ, A):
+    """The wave-group codes registered for this kv_idx tensor at this tile shape, or None."""
+    entry = _WAVE_BITS.get(id(kv_idx))
+    if entry is None or entry[0]() is not kv_idx:
+        return None
+    _, wave, bq, a = entry
+    return wave if (bq, a) == (BQ, A) and wave.shape == kv_idx.shape else None

@@ -1,0 +1,106 @@
+"""Disjoint split of a mask into sub-masks, one attention pass each, merged by log-sum-exp.
+
+The reference names this decomposition (src/polyattn/experiments/compose.py:7-17,
+docs/NOTES.md:355-363) and prices it (compose.py:107-119) but has no code for it.
+Here every piece is a (mask, tile shape, optional class-A permutation) and runs
+through pa_attn_fwd:
+
+* a piece with a permutation reads its Q/K/V rows through the permutation
+  (gather_q / gather_kv) and writes its output rows back to original positions
+  (scatter_o), so no permuted copy of Q, K, V or O is ever materialised;
+* the first pass writes O and the per-row LSE; every later pass merges its own
+  result with the previous one in its epilogue, in place (each output row is read
+  and written by the same lanes), so there is no separate merge pass.
+
+Pieces must be disjoint (the peeling of compose.py:49-76 makes them so); the merge
+of disjoint pieces equals single-pass attention over their union.
+"""
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from .attention import block_sparse_attention
+from .index import build_device
+from .polyattn.masks import Permuted
+from .spec import MaskSpec
+
+
+@dataclass
+class Piece:
+    mask: object                 # a polyattn mask object (its terms() give the predicate)
+    BQ: int = 128
+    A: int = 32
+    perm: Optional[object] = None  # index-space position -> original position (class-A basis)
+
+
+class SplitPlan:
+    """Block indices of every piece, built once on the GPU (offline, like
+    create_block_mask), then reused by every forward."""
+
+    def __init__(self, pieces, N, device=None):
+        self.N = N
+        self.pieces = list(pieces)
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.device = dev
+        self.built = []
+        for p in self.pieces:
+            perm_t = None
+            if p.perm is not None:
+                perm_t = (p.perm.to(device=dev, dtype=torch.int32) if isinstance(p.perm, torch.Tensor)
+                          else torch.from_numpy(np.asarray(p.perm, dtype=np.int32)).to(dev))
+            mask = Permuted(p.mask, perm_t.cpu().numpy()) if perm_t is not None else p.mask
+            kv_idx, kv_num, kv_partial, wave, tiles, live = build_device(mask, N, p.BQ, p.A, device=dev)
+            inc, exc = p.mask.terms()
+            order = None
+            self.built.append(dict(piece=p, spec=MaskSpec(tuple(inc), tuple(exc)), perm=perm_t,
+                                   kv_idx=kv_idx, kv_num=kv_num, kv_partial=kv_partial, wave=wave,
+                                   tiles=tiles, live=live, order=order))
+
+    @property
+    def live(self):
+        return sum(b["live"] for b in self.built)
+
+    @property
+    def elements(self):
+        return sum(b["tiles"] * b["piece"].BQ * b["piece"].A for b in self.built)
+
+    def forward(self, q, k, v, scale=None, out=None, lse=None):
+        """o [BH, N, D] in q's dtype; lse (float32 [BH, N]) receives the merged log-sum-exp."""
+        BH, N, D = q.shape
+        if N != self.N:
+            raise ValueError(f"plan built for N={self.N}, got N={N}")
+        o = out if out is not None else torch.empty_like(q)
+        lse_buf = lse if lse is not None else torch.empty((BH, N), dtype=torch.float32, device=q.device)
+        for i, b in enumerate(self.built):
+            p = b["piece"]
+            permuted = b["perm"] is not None
+            block_sparse_attention(
+                q, k, v, b["kv_idx"], b["kv_num"], b["kv_partial"], b["spec"], 0, 0, 0, p.BQ, p.A,
+                scale=scale, perm_q=b["perm"], perm_kv=b["perm"], gather_kv=permuted,
+                kv_wave_bits=b["wave"], gather_q=permuted, scatter_o=permuted,
+                lse=lse_buf, prev=None if i == 0 else (o, lse_buf), out=o, qblock_order=b["order"])
+        return o
+
+
+def lse_merge(o_parts, lse_parts, out_dtype=torch.float32, lse_out=None):
+    """Merge fp32 partials [BH, N, D] with their LSE [BH, N] (pa_lse_merge)."""
+    if not o_parts or len(o_parts) != len(lse_parts):
+        raise ValueError("need matching, non-empty o_parts and lse_parts")
+    o_parts = [t.contiguous() for t in o_parts]
+    lse_parts = [t.contiguous() for t in lse_parts]
+    _lib.require_device(*o_parts, *lse_parts)
+    BH, N, D = o_parts[0].shape
+    for o_, l_ in zip(o_parts, lse_parts):
+        if o_.dtype != torch.float32 or l_.dtype != torch.float32 or o_.shape != (BH, N, D) or l_.shape != (BH, N):
+            raise ValueError("parts must be float32 [BH, N, D] with float32 [BH, N] LSE")
+    out = torch.empty((BH, N, D), dtype=out_dtype, device=o_parts[0].device)
+    n = len(o_parts)
+    optrs = (_lib.c_vp * n)(*[t.data_ptr() for t in o_parts])
+    lptrs = (_lib.c_vp * n)(*[t.data_ptr() for t in lse_parts])
+    with torch.cuda.device(out.device):
+        _lib.check(_lib.lib().pa_lse_merge(optrs, lptrs, n, _lib.ptr(out), _lib.DTYPE_CODE[out_dtype],
+                                           _lib.ptr(lse_out), BH, N, D, _lib.stream_of(out)), "pa_lse_merge")
+    return out
