@@ -1,0 +1,206 @@
+#!/usr/bin/env python3
+"""Benchmark of the block-sparse masked attention forward on one MI355X.
+
+Default: the L=16384, H=32, D=128 bf16 workload (band-256 | lattice-16, split into
+band-256 in the identity basis and lattice-16 minus band in the rp16 basis, merged
+by log-sum-exp), inputs resident in HBM, one step = one forward over the batch.
+Prints ONE JSON line on stdout (the driver's contract); progress goes to stderr.
+
+  python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+  python bench.py --all [--report PATH]    every workload, a JSON report and a table
+
+The step times K back-to-back forwards between two device synchronisations.  HIP
+events around each kernel launch give the per-launch durations the roofline uses
+(live FLOPs of the launch / its duration, against the dense MFMA peak).  The CPU
+baseline times the oracle (gpu/reference.py restated: dense masked fp32 attention,
+torch on the host's cores) on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "block-sparse attn fwd ms + live-FLOP TFLOP/s (% bf16 MFMA peak), L=16k H=32 D=128"
+PEAK_TFLOPS = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}   # dense MFMA, MI355X
+HBM_GBPS = 8000.0
+# oracle predicate name of each workload's whole mask
+ORACLE_NAME = {"window128-L1k": "window-128", "dilated8-L8k": "dilated-8", "bandlat-L16k": "band256+lat16",
+               "sinkwin-L32k": "sinks64+win1024", "prefixlat-L64k": "prefixlm-2048"}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _dt(dtype):
+    import torch
+    return {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[dtype]
+
+
+def measure(plan_launches, steps, warmup):
+    """(wall ms per step, per-launch mean ms) over `steps` back-to-back forwards."""
+    import torch
+    for _ in range(warmup):
+        for launch in plan_launches:
+            launch()
+    torch.cuda.synchronize()
+    n = len(plan_launches)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        e = evs[s]
+        e[0].record()
+        for i, launch in enumerate(plan_launches):
+            launch()
+            e[i + 1].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    per = [sum(evs[s][i].elapsed_time(evs[s][i + 1]) for s in range(steps)) / steps for i in range(n)]
+    return wall_ms, per
+
+
+def cpu_baseline(wl, budget_s=12.0):
+    """Oracle dense fp32 attention on the host over (head, 1024-row chunk) units in
+    order until the budget is spent; live-FLOP TFLOP/s over what was processed."""
+    import torch
+
+    from oracle import attention as oatt
+    from oracle import masks as om
+    spec = om.NAMED[ORACLE_NAME[wl.name]]
+    q, k, v = (x.float() for x in wl.inputs(0, "cpu"))
+    chunk = 1024 if wl.L <= 32768 else 512
+    units = [(h, r0) for h in range(wl.H) for r0 in range(0, wl.L, chunk)]
+    live = 0
+    done = 0
+    t0 = time.perf_counter()
+    for h, r0 in units:
+        r1 = min(wl.L, r0 + chunk)
+        rows = om.rows(spec, r0, r1, wl.L)
+        oatt.dense_attention_torch(q[h:h + 1, r0:r1].contiguous(), k[h:h + 1], v[h:h + 1],
+                                   lambda a, b, rows=rows, r0=r0: rows[a - 0:b - 0], row_chunk=chunk)
+        live += int(rows.sum())
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    t = time.perf_counter() - t0
+    tflops = 4 * wl.D * live / t / 1e12
+    return dict(value=round(tflops, 6), unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{done} of {len(units)} (head, {chunk}-row) units of the same inputs, dense masked "
+                       f"fp32 attention over all {wl.L} keys (oracle, torch on the host), {t:.1f} s; "
+                       f"live pairs in the sample {live}")
+
+
+def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
+    import torch
+
+    from polyhedral_amd import workloads
+    from polyhedral_amd.split import SplitPlan
+    wl = workloads.make(name)
+    pieces = wl.variants[variant] if variant else wl.pieces
+    dev = torch.device(device)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan = SplitPlan(pieces, wl.L, dev)
+    torch.cuda.synchronize()
+    build_ms = (time.perf_counter() - t0) * 1e3
+    q, k, v = wl.inputs(0, dev)
+    launches, o, lse = plan.prepare(q, k, v)
+    wall_ms, per = measure(launches, steps, warmup)
+    live = plan.live
+    flops_live = 4 * wl.D * live * wl.H
+    flops_tile = 4 * wl.D * plan.elements * wl.H
+    kern_ms = sum(per)
+    dt = _dt(wl.dtype)
+    peak = PEAK_TFLOPS[dt]
+    achieved = flops_live / (kern_ms * 1e-3) / 1e12
+    res = dict(
+        workload=name + (f"[{variant}]" if variant else ""), description=wl.description, dtype=dt,
+        H=wl.H, L=wl.L, D=wl.D, live_pairs_per_head=live, tile_elements_per_head=plan.elements,
+        waste=round(plan.elements / live, 4) if live else None,
+        pieces=[dict(mask=b["piece"].mask.name, BQ=b["piece"].BQ, A=b["piece"].A,
+                     basis="identity" if b["perm"] is None else "permuted", tiles=b["tiles"], live=b["live"],
+                     launch_ms=round(per[i], 5),
+                     live_tflops=round(4 * wl.D * b["live"] * wl.H / (per[i] * 1e-3) / 1e12, 2) if per[i] else None)
+                for i, b in enumerate(plan.built)],
+        index_build_ms=round(build_ms, 2), ms_per_step=round(wall_ms, 5), kernel_ms=round(kern_ms, 5),
+        live_tflops=round(flops_live / (wall_ms * 1e-3) / 1e12, 3),
+        kernel_live_tflops=round(achieved, 3), tile_tflops=round(flops_tile / (kern_ms * 1e-3) / 1e12, 3),
+        peak_tflops=peak, frac_peak=round(achieved / peak, 4),
+        min_hbm_bytes=4 * wl.H * wl.L * wl.D * q.element_size(),
+    )
+    res["hbm_floor_ms"] = round(res["min_hbm_bytes"] / (HBM_GBPS * 1e9) * 1e3, 5)
+    res["_launches"] = len(launches)
+    if with_cpu:
+        log(f"[bench] cpu baseline for {name} ...")
+        res["cpu_baseline"] = cpu_baseline(wl)
+    del launches, o, lse, q, k, v, plan
+    torch.cuda.empty_cache()
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--variant", default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--all", action="store_true")
+    ap.add_argument("--report", default=None)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}). "
+              "The attention shards over heads with no exchange; run one process per GPU.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    from polyhedral_amd import workloads
+
+    if a.all:
+        rows = []
+        for name in workloads.NAMES:
+            wl = workloads.make(name)
+            for variant in [None] + list(wl.variants):
+                log(f"[bench] {name} {variant or ''}")
+                rows.append(run(name, a.steps, a.warmup, with_cpu=not a.no_cpu and variant is None,
+                                variant=variant))
+                r = rows[-1]
+                log(f"[bench]   {r['ms_per_step']:.4f} ms/step  kernel {r['kernel_ms']:.4f} ms  "
+                    f"{r['kernel_live_tflops']:.1f} live TFLOP/s ({100 * r['frac_peak']:.1f}% of {r['peak_tflops']})"
+                    f"  waste {r['waste']}")
+        out = dict(device=torch.cuda.get_device_name(0), results=rows)
+        if a.report:
+            with open(a.report, "w") as f:
+                json.dump(out, f, indent=1)
+        print(json.dumps(out))
+        return
+
+    name = a.workload or workloads.HEADLINE
+    r = run(name, a.steps, a.warmup, with_cpu=not a.no_cpu, variant=a.variant)
+    wl = workloads.make(name)
+    line = dict(
+        metric=METRIC, value=r["live_tflops"], unit="TFLOP/s", n_gpus=1, steps=a.steps, warmup=a.warmup,
+        ms_per_step=r["ms_per_step"], higher_is_better=True, scaling="weak", vs_baseline=None,
+        dtype=r["dtype"], data="synthetic",
+        config=dict(workload=r["workload"], description=wl.description, L=wl.L, H=wl.H, D=wl.D, B=1,
+                    live_pairs_per_head=r["live_pairs_per_head"], waste=r["waste"],
+                    pct_bf16_peak=round(100 * r["live_tflops"] / PEAK_TFLOPS["bf16"], 2),
+                    pieces=r["pieces"], index_build_ms=r["index_build_ms"]),
+        roofline=dict(bound="mfma", achieved=r["kernel_live_tflops"], peak=r["peak_tflops"], unit="TFLOP/s",
+                      frac=r["frac_peak"], traffic=None,
+                      kernel="attn_fwd_kernel (all launches of one step)",
+                      algorithmic="live FLOP = 4 * D * live pairs * heads per launch"),
+        cpu_baseline=r.get("cpu_baseline"),
+    )
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -97,6 +97,16 @@ int pa_index_compact(const uint32_t* tile_codes, const int32_t* kv_num, int64_t 
                      int32_t A, int32_t* kv_idx, int8_t* kv_partial, uint32_t* kv_wave_bits,
                      int64_t pitch, void* stream);
 
+/* Element bitmaps of the listed PARTIAL tiles, so the attention kernel masks from a
+ * table instead of evaluating the predicate.  part_base[i] = partial tiles listed in
+ * query blocks before i (exclusive prefix).  Writes kv_bits_off[i, j] = word offset of
+ * tile j's bitmap in `pool` (-1 for a full tile or padding) and, per partial tile,
+ * BQ rows x ceil(A/32) words: bit c of word w of row r = pair (row r, column 32 w + c)
+ * of the tile is live.  pool holds (total partial tiles) * BQ * ceil(A/32) words. */
+int pa_index_bits(const pa_mask* mask, int64_t N, int32_t BQ, int32_t A, const int32_t* kv_idx,
+                  const int32_t* kv_num, const int8_t* kv_partial, int64_t pitch,
+                  const int64_t* part_base, int32_t* kv_bits_off, uint32_t* pool, void* stream);
+
 /* ---- class-A permutation (replaces gpu/permute.py:12-31) -------------------------
  * Row gather dst[b, p, :] = src[b, perm[p], :] (inverse = 0), the index_select of
  * gpu/permute.py:22-24, or row scatter dst[b, perm[p], :] = src[b, p, :] (inverse = 1),
@@ -130,10 +140,15 @@ typedef struct pa_attn_args {
   const int8_t* kv_partial;     /* [N/BQ, pitch] */
   const uint32_t* kv_wave_bits; /* [N/BQ, pitch] or NULL: per-wave skip and mask bits */
   int64_t pitch;
+  const int32_t* kv_bits_off;   /* NULL, or pa_index_bits output: partial tiles are masked */
+  const uint32_t* kv_bits;      /*   from these bitmaps instead of evaluating `mask`       */
   pa_mask mask;   /* predicate applied on partial tiles, in original coordinates */
   int32_t gather_q;   /* load query rows through mask.perm_q (Q not physically permuted) */
   int32_t gather_kv;  /* load key/value rows through mask.perm_kv (gpu/triton_attn.py:104-107) */
   int32_t scatter_o;  /* store output row r at mask.perm_q[r] (fused inverse permutation) */
+  int32_t residue_s;      /* > 0: perm_q = perm_kv = the residue permutation of stride s     */
+  int32_t residue_qlog2;  /*   with N / s = 2^residue_qlog2, computed in closed form:        */
+                          /*   perm[p] = (p mod 2^qlog2) * s + p div 2^qlog2 (no table reads) */
   float* lse;         /* NULL or [BH, N] fp32, natural-log sum-exp of the stored rows */
   int64_t lse_sb;
   const void* prev_o;      /* NULL or a partial result over a disjoint sub-mask, same

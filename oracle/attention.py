@@ -76,3 +76,22 @@ def lse_merge(o_parts, lse_parts):
     o = np.where(den[..., None] > 0, o / np.where(den > 0, den, 1.0)[..., None], 0.0)
     lse = np.where(den > 0, mx + np.log(np.where(den > 0, den, 1.0)), -np.inf)
     return o, lse
+
+
+def dense_attention_torch(q, k, v, mask_rows, scale=None, row_chunk=1024):
+    """gpu/reference.py:5-13 in fp32 torch on the host, row-chunked: the CPU baseline.
+    q, k, v: CPU tensors [BH, N, D]; mask_rows(r0, r1) -> bool numpy [r1 - r0, N]."""
+    import torch
+    BH, N, D = q.shape
+    scale = scale or D ** -0.5
+    kf = k.float()
+    vf = v.float()
+    out = torch.empty((BH, N, D), dtype=torch.float32)
+    for r0 in range(0, N, row_chunk):
+        r1 = min(N, r0 + row_chunk)
+        m = torch.from_numpy(mask_rows(r0, r1))
+        s = (q[:, r0:r1].float() @ kf.transpose(-1, -2)) * scale
+        s = s.masked_fill(~m[None], float("-inf"))
+        p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
+        out[:, r0:r1] = p @ vf
+    return out

@@ -14,7 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libpolyattn_amd.s
 PA_OK, PA_E_INVALID, PA_E_HIP, PA_E_UNSUPPORTED = 0, -1, -2, -3
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 MAX_TERMS = 8
-ABI_VERSION = 1
+ABI_VERSION = 3
 
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -35,8 +35,9 @@ class PaAttnArgs(ctypes.Structure):
                 ("BH", c_i64), ("N", c_i64), ("D", c_i32), ("dtype", c_i32), ("scale", c_f32),
                 ("BQ", c_i32), ("A", c_i32),
                 ("kv_idx", c_vp), ("kv_num", c_vp), ("kv_partial", c_vp), ("kv_wave_bits", c_vp),
-                ("pitch", c_i64), ("mask", PaMask),
+                ("pitch", c_i64), ("kv_bits_off", c_vp), ("kv_bits", c_vp), ("mask", PaMask),
                 ("gather_q", c_i32), ("gather_kv", c_i32), ("scatter_o", c_i32),
+                ("residue_s", c_i32), ("residue_qlog2", c_i32),
                 ("lse", c_vp), ("lse_sb", c_i64),
                 ("prev_o", c_vp), ("prev_dtype", c_i32), ("prev_sb", c_i64), ("prev_sn", c_i64),
                 ("prev_lse", c_vp), ("qblock_order", c_vp)]
@@ -48,6 +49,8 @@ SIGNATURES = {
     "pa_abi_version": (c_i32, []),
     "pa_index_classify": (ctypes.c_int, [ctypes.POINTER(PaMask), c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "pa_index_compact": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "pa_index_bits": (ctypes.c_int, [ctypes.POINTER(PaMask), c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp,
+                                     c_vp, c_vp, c_vp]),
     "pa_permute_rows": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                        c_i32, c_vp]),
     "pa_invert_perm": (ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),

@@ -17,11 +17,14 @@ gfx950 kernel) instead of the Triton JIT.  Differences a caller can observe:
   raises NotImplementedError.
 
 Keyword-only extensions: kv_wave_bits (per-wave skip codes; found automatically for
-an index made by blockindex.build / to_cuda), gather_q / scatter_o (read Q rows
+an index made by blockindex.build / to_cuda), kv_bits (element bitmaps of the
+partial tiles from blockindex.build_device(bits=True): masking by table lookup,
+the predicate is then not evaluated), gather_q / scatter_o (read Q rows
 through perm_q and write O rows back to original positions: the class-A
 permutation fused into the kernel's loads and stores), lse (write the natural-log
 sum-exp per row), prev = (o_prev, lse_prev) (merge a partial over a disjoint
-sub-mask by log-sum-exp in the epilogue), out, qblock_order.
+sub-mask by log-sum-exp in the epilogue), out, qblock_order, residue (perm_q and
+perm_kv are residue_perm(N, residue): the kernel computes them in closed form).
 """
 import ctypes
 
@@ -54,17 +57,40 @@ def _rows3(t, name):
     return t
 
 
+class Launch:
+    """A validated pa_attn_fwd argument block and the tensors its pointers refer to.
+    __call__ launches it on the current stream of its device (no re-validation)."""
+
+    def __init__(self, args, keep, out, device):
+        self.args, self.keep, self.out, self.device = args, keep, out, device
+        self._ref = ctypes.byref(args)
+
+    def __call__(self):
+        _lib.check(_lib.lib().pa_attn_fwd(self._ref, _lib.stream_of(self.out)), "pa_attn_fwd")
+        return self.out
+
+
 def block_sparse_attention(q, k, v, kv_idx, kv_num, kv_partial,
                            kind, p0, p1, p2, BQ, A, scale=None,
                            perm_q=None, perm_kv=None, gather_kv=False,
                            gather_mult=1, gather_scatter=True,
-                           num_warps=4, num_stages=2, *,
-                           kv_wave_bits=None, gather_q=False, scatter_o=False,
-                           lse=None, prev=None, out=None, qblock_order=None):
+                           num_warps=4, num_stages=2, **ext):
     """q, k, v: [BH, N, D] (float32 / float16 / bfloat16). Returns o [BH, N, D], dtype of q.
 
     perm_q / perm_kv: int32 [N], permuted position -> ORIGINAL position, used to
     evaluate the mask in original coordinates (identity when None)."""
+    launch = prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale, perm_q, perm_kv,
+                     gather_kv, gather_mult, gather_scatter, num_warps, num_stages, **ext)
+    with torch.cuda.device(launch.device):
+        return launch()
+
+
+def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=None,
+            perm_q=None, perm_kv=None, gather_kv=False, gather_mult=1, gather_scatter=True,
+            num_warps=4, num_stages=2, *, kv_wave_bits=None, kv_bits=None, gather_q=False, scatter_o=False,
+            residue=0,
+            lse=None, prev=None, out=None, qblock_order=None):
+    """Validate the arguments of block_sparse_attention once and return a Launch."""
     BH, N, D = q.shape
     if perm_kv is None:
         perm_kv = perm_q
@@ -120,8 +146,20 @@ def block_sparse_attention(q, k, v, kv_idx, kv_num, kv_partial,
     args.kv_idx, args.kv_num, args.kv_partial = _lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial)
     args.kv_wave_bits = _lib.ptr(kv_wave_bits)
     args.pitch = kv_idx.shape[1]
+    if kv_bits is not None:
+        bits_off, bits_pool = kv_bits
+        _lib.require_device(bits_off, bits_pool)
+        if bits_off.shape != kv_idx.shape or bits_off.dtype != torch.int32 or bits_pool.dtype != torch.int32:
+            raise ValueError("kv_bits must be (int32 offsets shaped like kv_idx, int32 bitmap pool)")
+        args.kv_bits_off, args.kv_bits = _lib.ptr(bits_off), _lib.ptr(bits_pool)
     args.mask = dmask.struct()
     args.gather_q, args.gather_kv, args.scatter_o = int(bool(gather_q)), int(bool(gather_kv)), int(bool(scatter_o))
+    if residue:
+        # perm_q = perm_kv = residue_perm(N, residue), evaluated in closed form by the kernel
+        qn = N // residue
+        if N % residue or qn & (qn - 1):
+            raise ValueError(f"closed-form residue basis needs N/s a power of two (N={N}, s={residue})")
+        args.residue_s, args.residue_qlog2 = int(residue), qn.bit_length() - 1
     if lse is not None:
         _lib.require_device(lse)
         if lse.dtype != torch.float32 or lse.shape != (BH, N) or lse.stride(1) != 1:
@@ -146,6 +184,5 @@ def block_sparse_attention(q, k, v, kv_idx, kv_num, kv_partial,
         if qblock_order.numel() != nq:
             raise ValueError("qblock_order must have N/BQ entries")
         args.qblock_order = _lib.ptr(qblock_order)
-    with torch.cuda.device(dev):
-        _lib.check(_lib.lib().pa_attn_fwd(ctypes.byref(args), _lib.stream_of(q)), "pa_attn_fwd")
-    return o
+    keep = [q, k, v, o, kv_idx, kv_num, kv_partial, kv_wave_bits, kv_bits, dmask, lse, prev, qblock_order]
+    return Launch(args, keep, o, dev)

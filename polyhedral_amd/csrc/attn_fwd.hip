@@ -13,7 +13,9 @@ int launch_attn_f32(const AttnK& a, int D, int NW, hipStream_t s);
 extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   PA_CHECK_ARG(x != nullptr, "pa_attn_fwd: null args");
   PA_CHECK_ARG(x->q && x->k && x->v && x->o, "pa_attn_fwd: null q/k/v/o");
-  PA_CHECK_ARG(x->kv_idx && x->kv_num && x->kv_partial, "pa_attn_fwd: null block index");
+  PA_CHECK_ARG(x->kv_num, "pa_attn_fwd: null kv_num");
+  // an index whose every list is empty has pitch 0 and no list storage
+  PA_CHECK_ARG(x->pitch == 0 || (x->kv_idx && x->kv_partial), "pa_attn_fwd: null kv_idx / kv_partial");
   PA_CHECK_ARG(x->D == 64 || x->D == 128, "pa_attn_fwd: D=%d (supported: 64, 128)", x->D);
   PA_CHECK_ARG(x->dtype == PA_F32 || x->dtype == PA_F16 || x->dtype == PA_BF16, "pa_attn_fwd: dtype %d",
                x->dtype);
@@ -25,9 +27,17 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   PA_CHECK_ARG(x->N % x->BQ == 0 && x->N % x->A == 0, "pa_attn_fwd: N=%lld not divisible by BQ=%d, A=%d",
                (long long)x->N, x->BQ, x->A);
   PA_CHECK_ARG(x->pitch >= 0, "pa_attn_fwd: negative pitch");
-  PA_CHECK_ARG(!(x->gather_q || x->scatter_o) || x->mask.perm_q,
-               "pa_attn_fwd: gather_q / scatter_o need mask.perm_q");
-  PA_CHECK_ARG(!x->gather_kv || x->mask.perm_kv, "pa_attn_fwd: gather_kv needs mask.perm_kv");
+  PA_CHECK_ARG(x->pitch == 0 || !x->kv_bits_off == !x->kv_bits,
+               "pa_attn_fwd: kv_bits_off and kv_bits go together");
+  PA_CHECK_ARG(x->residue_s <= 0 ||
+                   (x->residue_qlog2 >= 0 && x->residue_qlog2 < 31 &&
+                    (int64_t)x->residue_s << x->residue_qlog2 == x->N),
+               "pa_attn_fwd: residue_s=%d with N/s = 2^%d does not match N=%lld", x->residue_s,
+               x->residue_qlog2, (long long)x->N);
+  PA_CHECK_ARG(!(x->gather_q || x->scatter_o) || x->mask.perm_q || x->residue_s > 0,
+               "pa_attn_fwd: gather_q / scatter_o need mask.perm_q or residue_s");
+  PA_CHECK_ARG(!x->gather_kv || x->mask.perm_kv || x->residue_s > 0,
+               "pa_attn_fwd: gather_kv needs mask.perm_kv or residue_s");
   PA_CHECK_ARG(!x->prev_o || x->prev_lse, "pa_attn_fwd: prev_o needs prev_lse");
   PA_CHECK_ARG(!x->prev_o || x->prev_dtype == PA_F32 || x->prev_dtype == PA_F16 || x->prev_dtype == PA_BF16,
                "pa_attn_fwd: prev_dtype %d", x->prev_dtype);
@@ -55,6 +65,7 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   a.N = (int32_t)x->N;
   a.BQ = x->BQ;
   a.A = x->A;
+  a.spt_log2 = x->A == 16 ? 0 : x->A == 32 ? 1 : x->A == 64 ? 2 : 3;
   a.nq = (int32_t)(x->N / x->BQ);
   a.total_wg = (int64_t)a.nq * x->BH;
   a.c = x->scale * 1.4426950408889634f;
@@ -63,10 +74,14 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   a.kv_partial = x->kv_partial;
   a.kv_wave_bits = x->kv_wave_bits;
   a.pitch = x->pitch;
+  a.kv_bits_off = x->kv_bits_off;
+  a.kv_bits = x->kv_bits;
   a.pred = pa::make_pred(x->mask);
   a.gather_q = x->gather_q;
   a.gather_kv = x->gather_kv;
   a.scatter_o = x->scatter_o;
+  a.residue_s = x->residue_s > 0 ? x->residue_s : 0;
+  a.residue_qlog2 = x->residue_s > 0 ? x->residue_qlog2 : 0;
   a.lse = x->lse;
   a.lse_sb = x->lse_sb;
   a.prev_o = static_cast<const char*>(x->prev_o);

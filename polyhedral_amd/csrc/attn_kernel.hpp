@@ -17,11 +17,15 @@
 //    buffered, the next step's global loads in flight while this one computes.
 //    K rows are stored with a 16-B XOR swizzle; V is stored transposed (V^T) for
 //    the bf16/f16 MFMA A operand, in the KV-slot order that matches P^T's.
+//  * Everything a step needs to know about its segments (tile row, wave codes,
+//    bitmap offset) is read with uniform (scalar) loads two steps ahead, and a
+//    residue-class permutation is evaluated in closed form, so no global load
+//    depends on another inside the loop.
 //  * Per-wave skip: the tile codes (2 bits per 32-row x 32-column wave group)
-//    let a wave skip MFMA work on a 32x32 block that is dead for its rows, and
-//    apply the element predicate only to blocks that are not full for its rows.
-//    A full tile costs no predicate work at all (the reference masks every tile,
-//    gpu/triton_attn.py:140-167).
+//    let a wave skip MFMA work on a 32x32 block that is dead for its rows and
+//    mask only blocks that are not full for its rows.  Partial segments are
+//    masked from element bitmaps staged into LDS with K and V, or, without
+//    bitmaps, by evaluating the predicate in a compact loop.
 //  * Lazy rescaling: the running max m is raised only when a row's new max
 //    exceeds it by more than 8 (log2 units); the result is identical in exact
 //    arithmetic and the wave skips the O rescale on most steps.
@@ -47,6 +51,7 @@ struct AttnK {
   char* o;
   int64_t q_sb, q_sn, k_sb, k_sn, v_sb, v_sn, o_sb, o_sn;  // element strides
   int32_t N, BQ, A, nq;
+  int32_t spt_log2;  // log2(A / 16): 16-row segments per tile
   int64_t total_wg;
   float c;  // scale * log2(e)
   const int32_t* kv_idx;
@@ -54,8 +59,11 @@ struct AttnK {
   const int8_t* kv_partial;
   const uint32_t* kv_wave_bits;
   int64_t pitch;
+  const int32_t* kv_bits_off;
+  const uint32_t* kv_bits;
   Pred pred;
   int32_t gather_q, gather_kv, scatter_o;
+  int32_t residue_s, residue_qlog2;
   float* lse;
   int64_t lse_sb;
   const char* prev_o;
@@ -115,13 +123,24 @@ __device__ __forceinline__ f32x4 load4_any(const char* p, int32_t dt) {
 
 __device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32, 64); }
 
-// Segment status for one wave: some pair live / every pair live (invalid -> 0, 0).
-struct SegStat {
-  bool any, all;
+// Uniform description of the 4 segments of one step.
+struct StepMeta {
+  int32_t base[4];   // index-space KV row of the segment's first row; -1 past the list
+  uint32_t code[4];  // tile code shifted to the segment's column group (0 past the list)
+  int32_t boff[4];   // bitmap word offset of the segment's tile (-1: none)
 };
 
+// Two waves per SIMD where the registers allow it (4-wave work-groups, except fp32 with
+// D = 128): two work-groups then share a CU, one computing while the other waits on its
+// K/V loads.  The 1- and 2-wave shapes (BQ <= 64) stage more rows per thread and keep one.
 template <typename T, int D, int NW>
-__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
+constexpr int occupancy_target() {
+  return (NW == 4 && (sizeof(T) == 2 || D == 64)) ? 2 : 1;
+}
+
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_target<T, D, NW>())))
+void attn_fwd_kernel(const AttnK a) {
   constexpr bool kF32 = sizeof(T) == 4;
   constexpr int ESZ = sizeof(T);
   constexpr int UPR = D * ESZ / 16;                 // 16-B units per row
@@ -133,9 +152,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
   constexpr int VT = kF32 ? 0 : (VTASKS + NT - 1) / NT;
   constexpr int VU = kF32 ? KU : 1;                 // f32: V staged like K
   constexpr int NDB = D / 32;                       // 32-wide output blocks
+  constexpr int ROWS = NW * 32;                     // query rows held by the work-group
+  constexpr int BW = (4 * ROWS + NT - 1) / NT;      // bitmap words staged per thread
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
   __shared__ int32_t kvo_s[2][kStep];
+  __shared__ uint32_t bits_s[2][4][ROWS];
+  __shared__ pa_term terms_s[PA_MAX_TERMS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -149,21 +172,35 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
   const int qb = a.qblock_order ? a.qblock_order[qb_lin] : qb_lin;
 
   const int A = a.A;
-  const int spt = A >> 4;                  // 16-row segments per tile
+  const int spt_log2 = a.spt_log2;
+  const int spt_mask = (1 << spt_log2) - 1;
   const int ncg = A >= 32 ? (A >> 5) : 1;  // wave column groups per tile
   const int64_t row0 = (int64_t)qb * a.pitch;
-  const int n_seg = a.kv_num[qb] * spt;
+  const int n_seg = a.kv_num[qb] << spt_log2;
   const int n_steps = (n_seg + 3) >> 2;
+  const bool use_bits = a.kv_bits != nullptr;
+
+  // index-space position -> original position
+  const int32_t rmask = (1 << a.residue_qlog2) - 1;
+  auto orig_q = [&](int p) -> int {
+    if (a.residue_s) return (p & rmask) * a.residue_s + (p >> a.residue_qlog2);
+    return a.pred.perm_q ? a.pred.perm_q[p] : p;
+  };
+  auto orig_kv = [&](int p) -> int {
+    if (a.residue_s) return (p & rmask) * a.residue_s + (p >> a.residue_qlog2);
+    return a.pred.perm_kv ? a.pred.perm_kv[p] : p;
+  };
+  const bool has_pq = a.residue_s || a.pred.perm_q;
+  const bool gather_kv = a.gather_kv && (a.residue_s || a.pred.perm_kv);
 
   const int rows_valid = a.BQ < 32 ? a.BQ : 32;
   const bool q_ok = m < rows_valid;
   const int r_idx = qb * a.BQ + w * 32 + m;  // index-space query row of this lane
-  int q_orig = r_idx, r_load = r_idx;
-  if (q_ok && a.pred.perm_q) {
-    q_orig = a.pred.perm_q[r_idx];
-    if (a.gather_q) r_load = q_orig;
+  int q_orig = 0, r_load = r_idx;
+  if (q_ok) {
+    q_orig = has_pq ? orig_q(r_idx) : r_idx;
+    if (a.gather_q && has_pq) r_load = q_orig;
   }
-  if (!q_ok) q_orig = 0;
 
   // ---- Q fragment (B operand of S^T = K Q^T) -------------------------------
   using QFrag = typename Mma<T>::frag;
@@ -199,33 +236,56 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
   const char* kbase = a.k + bh * a.k_sb * ESZ;
   const char* vbase = a.v + bh * a.v_sb * ESZ;
 
+  // ---- per-step metadata (uniform, scalar loads) -----------------------------
+  auto step_meta = [&](int j) -> StepMeta {
+    StepMeta mt;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int seg = 4 * j + t;
+      mt.base[t] = -1;
+      mt.code[t] = 0u;
+      mt.boff[t] = -1;
+      if (seg < n_seg) {
+        const int64_t ti = row0 + (seg >> spt_log2);
+        const int within = seg & spt_mask;
+        mt.base[t] = a.kv_idx[ti] * A + within * 16;
+        if (a.kv_wave_bits) {
+          const int cg = A >= 32 ? (within >> 1) : 0;
+          mt.code[t] = a.kv_wave_bits[ti] >> (2 * cg);
+        } else {
+          mt.code[t] = a.kv_partial[ti] ? 0x55555555u : 0xffffffffu;
+        }
+        if (use_bits) mt.boff[t] = a.kv_bits_off[ti];
+      }
+    }
+    return mt;
+  };
+  auto seg_base = [](const StepMeta& mt, int r) -> int {
+    const int t = r >> 4;
+    return t == 0 ? mt.base[0] : t == 1 ? mt.base[1] : t == 2 ? mt.base[2] : mt.base[3];
+  };
+
   // ---- staging ------------------------------------------------------------
   uint4 kreg[KU];
   uint4 vreg[kF32 ? VU : VT][kF32 ? 1 : 4];
+  uint32_t breg[BW];
 
-  // KV row (index space) of local row r of step j, or -1 if its segment is past the list.
-  auto kv_row = [&](int j, int r) -> int {
-    const int seg = 4 * j + (r >> 4);
-    if (seg >= n_seg) return -1;
-    const int tile = a.kv_idx[row0 + seg / spt];
-    return tile * A + (seg % spt) * 16 + (r & 15);
-  };
-  auto load_row_of = [&](int kvr) -> int {
-    return (a.gather_kv && a.pred.perm_kv) ? a.pred.perm_kv[kvr] : kvr;
+  auto load_row = [&](const StepMeta& mt, int r) -> int {  // global row, or -1
+    const int b0 = seg_base(mt, r);
+    if (b0 < 0) return -1;
+    const int kvr = b0 + (r & 15);
+    return gather_kv ? orig_kv(kvr) : kvr;
   };
 
-  auto load_step = [&](int j) {
+  auto load_step = [&](const StepMeta& mt) {
 #pragma unroll
     for (int i = 0; i < KU; ++i) {
       const int u = tid + i * NT;
       kreg[i] = uint4{0, 0, 0, 0};
       if (u < kStep * UPR) {
         const int r = u / UPR, un = u % UPR;
-        const int kvr = kv_row(j, r);
-        if (kvr >= 0) {
-          const int lr = load_row_of(kvr);
-          kreg[i] = *reinterpret_cast<const uint4*>(kbase + ((int64_t)lr * a.k_sn) * ESZ + un * 16);
-        }
+        const int lr = load_row(mt, r);
+        if (lr >= 0) kreg[i] = *reinterpret_cast<const uint4*>(kbase + ((int64_t)lr * a.k_sn) * ESZ + un * 16);
       }
     }
     if constexpr (kF32) {
@@ -235,11 +295,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
         vreg[i][0] = uint4{0, 0, 0, 0};
         if (u < kStep * UPR) {
           const int r = u / UPR, un = u % UPR;
-          const int kvr = kv_row(j, r);
-          if (kvr >= 0) {
-            const int lr = load_row_of(kvr);
+          const int lr = load_row(mt, r);
+          if (lr >= 0)
             vreg[i][0] = *reinterpret_cast<const uint4*>(vbase + ((int64_t)lr * a.v_sn) * ESZ + un * 16);
-          }
         }
       }
     } else {
@@ -255,12 +313,25 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
           const int rbase = 16 * (g >> 2) + 4 * (((gg & 1) << 1) | (gg >> 1));
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int kvr = kv_row(j, rbase + e);
-            if (kvr >= 0) {
-              const int lr = load_row_of(kvr);
+            const int lr = load_row(mt, rbase + e);
+            if (lr >= 0)
               vreg[i][e] = *reinterpret_cast<const uint4*>(vbase + ((int64_t)lr * a.v_sn) * ESZ + un * 16);
-            }
           }
+        }
+      }
+    }
+    if (use_bits) {
+      const int wpr = (A + 31) >> 5;
+#pragma unroll
+      for (int i = 0; i < BW; ++i) {
+        const int x = tid + i * NT;
+        breg[i] = 0u;
+        if (x < 4 * ROWS) {
+          const int t = x / ROWS, rr = x % ROWS;
+          const int off = t == 0 ? mt.boff[0] : t == 1 ? mt.boff[1] : t == 2 ? mt.boff[2] : mt.boff[3];
+          const int sb = t == 0 ? mt.base[0] : t == 1 ? mt.base[1] : t == 2 ? mt.base[2] : mt.base[3];
+          const int col = sb & (A - 1);  // first column of the segment inside its tile
+          if (off >= 0 && rr < a.BQ) breg[i] = a.kv_bits[(int64_t)off + rr * wpr + (col >> 5)] >> (col & 31);
         }
       }
     }
@@ -268,7 +339,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
 
   auto ksw = [](int r) -> int { return UPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
 
-  auto store_step = [&](int j, int b) {
+  auto store_step = [&](const StepMeta& mt, int b) {
     char* Ks = smem + b * BUF_BYTES;
     char* Vs = Ks + K_BYTES;
 #pragma unroll
@@ -295,63 +366,84 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
         const int t = tid + i * NT;
         if (t < VTASKS) {
           const int g = t / UPR, un = t % UPR;
-          const uint16_t* r0 = reinterpret_cast<const uint16_t*>(&vreg[i][0]);
-          const uint16_t* r1 = reinterpret_cast<const uint16_t*>(&vreg[i][1]);
-          const uint16_t* r2 = reinterpret_cast<const uint16_t*>(&vreg[i][2]);
-          const uint16_t* r3 = reinterpret_cast<const uint16_t*>(&vreg[i][3]);
+          // 16-bit element e of a 16-B unit: word e / 2, half e % 2 (no address taken,
+          // so the staging registers never go to scratch)
+          auto half = [](const uint4& u, int e) -> uint32_t {
+            const uint32_t wv = e < 2 ? u.x : e < 4 ? u.y : e < 6 ? u.z : u.w;
+            return (e & 1) ? (wv >> 16) : (wv & 0xffffu);
+          };
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int d = 8 * un + e;
             uint2 val;
-            val.x = (uint32_t)r0[e] | ((uint32_t)r1[e] << 16);
-            val.y = (uint32_t)r2[e] | ((uint32_t)r3[e] << 16);
+            val.x = half(vreg[i][0], e) | (half(vreg[i][1], e) << 16);
+            val.y = half(vreg[i][2], e) | (half(vreg[i][3], e) << 16);
             const int unit = (g >> 1) ^ ((d >> 1) & 7);
             *reinterpret_cast<uint2*>(Vs + d * 128 + unit * 16 + (g & 1) * 8) = val;
           }
         }
       }
     }
-    if (tid < kStep) {
-      const int kvr = kv_row(j, tid);
-      kvo_s[b][tid] = kvr < 0 ? -1 : (a.pred.perm_kv ? a.pred.perm_kv[kvr] : kvr);
+    if (use_bits) {
+#pragma unroll
+      for (int i = 0; i < BW; ++i) {
+        const int x = tid + i * NT;
+        if (x < 4 * ROWS) bits_s[b][x / ROWS][x % ROWS] = breg[i];
+      }
+    } else if (tid < kStep) {
+      // predicate path: original KV coordinate of every staged row
+      const int b0 = seg_base(mt, tid);
+      kvo_s[b][tid] = b0 < 0 ? -1 : orig_kv(b0 + (tid & 15));
     }
   };
 
-  auto seg_stat = [&](int seg) -> SegStat {
-    if (seg >= n_seg) return SegStat{false, false};
-    const int64_t ti = row0 + seg / spt;
-    if (a.kv_wave_bits) {
-      const uint32_t code = a.kv_wave_bits[ti];
-      const int cg = A >= 32 ? ((seg % spt) >> 1) : 0;
-      const int g = w * ncg + cg;
-      return SegStat{((code >> (2 * g)) & 1u) != 0u, ((code >> (2 * g + 1)) & 1u) != 0u};
+  // 8 live bits for elements 8h..8h+7 of block lb (segment t = 2 lb + h), a segment
+  // that is partial for this wave.  Element e sits at segment row 8 * (e / 4) + 4 * G + e % 4.
+  auto seg_live8 = [&](int b, int lb, int h) -> uint32_t {
+    if (use_bits) {
+      const uint32_t field = q_ok ? bits_s[b][2 * lb + h][w * 32 + m] : 0u;
+      return ((field >> (4 * G)) & 0xfu) | (((field >> (8 + 4 * G)) & 0xfu) << 4);
     }
-    return SegStat{true, a.kv_partial[ti] == 0};
+    uint32_t bits = 0u;
+#pragma unroll 1
+    for (int e = 0; e < 8; ++e) {
+      const int ko = kvo_s[b][32 * lb + 16 * h + 8 * (e >> 2) + 4 * G + (e & 3)];
+      if (ko >= 0 && pred_live_rolled(terms_s, a.pred.n_include, a.pred.n_exclude, q_orig, ko,
+                                      a.pred.dense_bits, a.pred.dense_words))
+        bits |= 1u << e;
+    }
+    return bits;
   };
 
   // ---- main loop ------------------------------------------------------------
+#pragma unroll
+  for (int i = 0; i < PA_MAX_TERMS; ++i)  // constant indices into the argument block
+    if (tid == i) terms_s[i] = a.pred.terms[i];
+  StepMeta m_cur = step_meta(0);
+  StepMeta m_nxt = step_meta(1);
   if (n_steps > 0) {
-    load_step(0);
-    store_step(0, 0);
+    load_step(m_cur);
+    store_step(m_cur, 0);
   }
   __syncthreads();
 
+  const int gshift = 2 * w * ncg;  // this wave's group inside a (shifted) tile code
   for (int j = 0; j < n_steps; ++j) {
     const int b = j & 1;
     const bool more = j + 1 < n_steps;
-    if (more) load_step(j + 1);
+    const StepMeta m_after = step_meta(j + 2);  // scalar loads, in flight during this step
+    if (more) load_step(m_nxt);
 
     const char* Ks = smem + b * BUF_BYTES;
     const char* Vs = Ks + K_BYTES;
-    const int32_t* kvo = kvo_s[b];
 
     f32x16 s[2];
     bool blive[2];
 #pragma unroll
     for (int lb = 0; lb < 2; ++lb) {
-      const SegStat st0 = seg_stat(4 * j + 2 * lb);
-      const SegStat st1 = seg_stat(4 * j + 2 * lb + 1);
-      blive[lb] = st0.any || st1.any;
+      const uint32_t c0 = m_cur.code[2 * lb] >> gshift, c1 = m_cur.code[2 * lb + 1] >> gshift;
+      const bool any0 = c0 & 1u, all0 = (c0 >> 1) & 1u, any1 = c1 & 1u, all1 = (c1 >> 1) & 1u;
+      blive[lb] = any0 || any1;
       s[lb] = f32x16{0};
       if (!blive[lb]) continue;
       // S^T block: rows = 32 KV rows of this block, cols = the wave's 32 query rows
@@ -375,22 +467,14 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
           s[lb] = Mma<T>::mma(__builtin_bit_cast(typename Mma<T>::frag, kx), qf[kc], s[lb]);
         }
       }
-      if (!(st0.all && st1.all)) {
+      if (!(all0 && all1)) {
+        // live bit i <-> s[lb][i]; a segment is full, dead, or looked up / evaluated
+        const uint32_t lo = all0 ? 0xffu : (any0 ? seg_live8(b, lb, 0) : 0u);
+        const uint32_t hi = all1 ? 0xffu : (any1 ? seg_live8(b, lb, 1) : 0u);
+        const uint32_t live = lo | (hi << 8);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const SegStat st = h ? st1 : st0;
-          if (st.all) continue;
-#pragma unroll
-          for (int i = 8 * h; i < 8 * h + 8; ++i) {
-            bool live = false;
-            if (st.any) {
-              const int r = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
-              const int ko = kvo[r];
-              live = ko >= 0 && pred_live(a.pred, q_orig, ko);
-            }
-            if (!live) s[lb][i] = -INFINITY;
-          }
-        }
+        for (int i = 0; i < 16; ++i)
+          if (!((live >> i) & 1u)) s[lb][i] = -INFINITY;
       }
     }
 
@@ -454,7 +538,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
       }
     }
 
-    if (more) store_step(j + 1, b ^ 1);
+    if (more) store_step(m_nxt, b ^ 1);
+    m_cur = m_nxt;
+    m_nxt = m_after;
     __syncthreads();
   }
 
@@ -464,7 +550,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const AttnK a) {
   float lse_v = has ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
   float a_own = has ? 1.f / l_tot : 0.f;  // weight on acc
   float a_prev = 0.f;
-  const int srow = (a.scatter_o && a.pred.perm_q) ? q_orig : r_idx;
+  const int srow = (a.scatter_o && has_pq) ? q_orig : r_idx;
   if (a.prev_o && q_ok) {
     const float lp = a.prev_lse[bh * a.lse_sb + srow];
     const float M = fmaxf(lse_v, lp);

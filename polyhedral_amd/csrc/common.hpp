@@ -80,13 +80,41 @@ __device__ __forceinline__ bool term_live(const pa_term& t, int32_t q, int32_t k
   }
 }
 
+// Unrolled over the fixed term capacity so every terms[i] access has a constant
+// index: a runtime index would make the compiler copy the whole kernel-argument
+// block into scratch memory.
 __device__ __forceinline__ bool pred_live(const Pred& p, int32_t q, int32_t kv) {
-  bool inc = false;
-  for (int i = 0; i < p.n_include; ++i) inc |= term_live(p.terms[i], q, kv, p.dense_bits, p.dense_words);
-  if (!inc) return false;
-  for (int i = 0; i < p.n_exclude; ++i)
-    if (term_live(p.terms[p.n_include + i], q, kv, p.dense_bits, p.dense_words)) return false;
-  return true;
+  bool inc = false, exc = false;
+  const int n = p.n_include + p.n_exclude;
+#pragma unroll
+  for (int i = 0; i < PA_MAX_TERMS; ++i) {
+    if (i < n) {
+      const bool l = term_live(p.terms[i], q, kv, p.dense_bits, p.dense_words);
+      if (i < p.n_include)
+        inc |= l;
+      else
+        exc |= l;
+    }
+  }
+  return inc && !exc;
+}
+
+// Same predicate with the terms read from memory (LDS in the attention kernel) in a
+// rolled loop: one copy of the term switch, for code that evaluates it rarely.
+__device__ __forceinline__ bool pred_live_rolled(const pa_term* terms, int n_include, int n_exclude,
+                                                 int32_t q, int32_t kv, const uint32_t* dense,
+                                                 int64_t words) {
+  bool inc = false, exc = false;
+#pragma unroll 1
+  for (int i = 0; i < n_include + n_exclude; ++i) {
+    const pa_term t = terms[i];
+    const bool l = term_live(t, q, kv, dense, words);
+    if (i < n_include)
+      inc |= l;
+    else
+      exc |= l;
+  }
+  return inc && !exc;
 }
 
 // Validates a host-side pa_mask; returns 0 or an error code (message set).

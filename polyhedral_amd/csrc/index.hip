@@ -210,3 +210,74 @@ extern "C" int pa_index_compact(const uint32_t* tile_codes, const int32_t* kv_nu
   PA_LAUNCH_CHECK("compact_kernel");
   return PA_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Element bitmaps of the listed partial tiles (phase 3).  One work-group per query
+// block walks its list; each partial tile gets BQ x ceil(A/32) words, one thread per
+// word, 32 predicate evaluations per word.
+namespace pa {
+namespace {
+
+__global__ __launch_bounds__(kThreads) void bits_kernel(const Pred pred, int32_t N, int32_t BQ, int32_t A,
+                                                         const int32_t* __restrict__ kv_idx,
+                                                         const int32_t* __restrict__ kv_num,
+                                                         const int8_t* __restrict__ kv_partial, int64_t pitch,
+                                                         const int64_t* __restrict__ part_base,
+                                                         int32_t* __restrict__ kv_bits_off,
+                                                         uint32_t* __restrict__ pool) {
+  __shared__ int32_t q_orig[128];
+  const int tid = threadIdx.x;
+  const int qb = blockIdx.x;
+  const int wpr = (A + 31) >> 5;
+  const int words = BQ * wpr;
+  if (tid < BQ) {
+    const int r = qb * BQ + tid;
+    q_orig[tid] = pred.perm_q ? pred.perm_q[r] : r;
+  }
+  __syncthreads();
+  const int n = kv_num[qb];
+  const int64_t row = (int64_t)qb * pitch;
+  int64_t rank = part_base[qb];
+  for (int j = 0; j < n; ++j) {
+    const bool partial = kv_partial[row + j] != 0;
+    if (tid == 0) kv_bits_off[row + j] = partial ? (int32_t)(rank * words) : -1;
+    if (!partial) continue;
+    const int kb = kv_idx[row + j];
+    uint32_t* dst = pool + rank * words;
+    for (int wi = tid; wi < words; wi += kThreads) {
+      const int rr = wi / wpr, cw = wi % wpr;
+      const int c0 = kb * A + cw * 32;
+      const int ncol = A - cw * 32 < 32 ? A - cw * 32 : 32;
+      uint32_t bits = 0u;
+      for (int c = 0; c < ncol; ++c) {
+        const int col = c0 + c;
+        const int32_t ko = pred.perm_kv ? pred.perm_kv[col] : col;
+        bits |= (pred_live(pred, q_orig[rr], ko) ? 1u : 0u) << c;
+      }
+      dst[wi] = bits;
+    }
+    ++rank;
+  }
+  for (int64_t j = n + tid; j < pitch; j += kThreads) kv_bits_off[row + j] = -1;
+}
+
+}  // namespace
+}  // namespace pa
+
+extern "C" int pa_index_bits(const pa_mask* mask, int64_t N, int32_t BQ, int32_t A, const int32_t* kv_idx,
+                             const int32_t* kv_num, const int8_t* kv_partial, int64_t pitch,
+                             const int64_t* part_base, int32_t* kv_bits_off, uint32_t* pool, void* stream) {
+  PA_CHECK_ARG(mask && kv_num && part_base, "pa_index_bits: null argument");
+  PA_CHECK_ARG(N >= 1 && N <= (1ll << 30), "pa_index_bits: N=%lld out of range", (long long)N);
+  PA_CHECK_ARG(pa::tile_ok(BQ) && pa::tile_ok(A) && N % BQ == 0 && N % A == 0,
+               "pa_index_bits: bad tile shape BQ=%d A=%d for N=%lld", BQ, A, (long long)N);
+  if (pitch == 0) return PA_OK;
+  PA_CHECK_ARG(kv_idx && kv_partial && kv_bits_off, "pa_index_bits: null list");
+  if (int rc = pa::check_mask(mask, N)) return rc;
+  const pa::Pred pred = pa::make_pred(*mask);
+  hipLaunchKernelGGL(pa::bits_kernel, dim3((unsigned)(N / BQ)), dim3(pa::kThreads), 0,
+                     static_cast<hipStream_t>(stream), pred, (int32_t)N, BQ, A, kv_idx, kv_num, kv_partial,
+                     pitch, part_base, kv_bits_off, pool);
+  PA_LAUNCH_CHECK("bits_kernel");
+  return PA_OK;
+}

@@ -71,9 +71,12 @@ def _default_device(device):
     return torch.device(device)
 
 
-def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None):
+def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None, bits=False):
     """Build on the GPU; returns (kv_idx, kv_num, kv_partial, kv_wave_bits, tiles, live) with
-    device tensors and host ints.  One synchronisation (to size the padded lists)."""
+    device tensors and host ints.  One synchronisation (to size the padded lists).
+
+    bits=True appends (kv_bits_off, kv_bits): element bitmaps of the partial tiles
+    (pa_index_bits), so the attention kernel masks by table lookup."""
     assert N % BQ == 0 and N % A == 0
     dev = _default_device(device)
     dm = device_mask(mask, N, dev, perm=perm, perm_kv=perm_kv)
@@ -94,8 +97,20 @@ def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None):
         _lib.check(L.pa_index_compact(_lib.ptr(codes), _lib.ptr(kv_num), N, BQ, A, _lib.ptr(kv_idx),
                                       _lib.ptr(kv_partial), _lib.ptr(wave), max_kv, stream),
                    "pa_index_compact")
+        out = (kv_idx, kv_num, kv_partial, wave, tiles, live)
+        if bits:
+            part = kv_partial.to(torch.int64).sum(1)
+            part_base = torch.cumsum(part, 0) - part
+            n_part = int(part.sum())
+            wpr = (A + 31) // 32
+            pool = torch.zeros(max(1, n_part * BQ * wpr), dtype=torch.int32, device=dev)
+            off = torch.full((nq, max_kv), -1, dtype=torch.int32, device=dev)
+            _lib.check(L.pa_index_bits(ctypes.byref(ms), N, BQ, A, _lib.ptr(kv_idx), _lib.ptr(kv_num),
+                                       _lib.ptr(kv_partial), max_kv, _lib.ptr(part_base), _lib.ptr(off),
+                                       _lib.ptr(pool), stream), "pa_index_bits")
+            out = out + ((off, pool),)
     _register_wave_bits(kv_idx, wave, BQ, A)
-    return kv_idx, kv_num, kv_partial, wave, tiles, live
+    return out
 
 
 def build(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None):

@@ -22,8 +22,9 @@ import numpy as np
 import torch
 
 from . import _lib
-from .attention import block_sparse_attention
+from .attention import prepare
 from .index import build_device
+from .perm import residue_perm
 from .polyattn.masks import Permuted
 from .spec import MaskSpec
 
@@ -34,13 +35,21 @@ class Piece:
     BQ: int = 128
     A: int = 32
     perm: Optional[object] = None  # index-space position -> original position (class-A basis)
+    residue: int = 0               # > 0: the basis is residue_perm(N, residue) (perm may be omitted)
+
+
+def _closed_form_residue(piece, N):
+    """The piece's residue stride if the kernel can evaluate its basis in closed form."""
+    s = piece.residue
+    return s if s and N % s == 0 and ((N // s) & (N // s - 1)) == 0 else 0
 
 
 class SplitPlan:
     """Block indices of every piece, built once on the GPU (offline, like
-    create_block_mask), then reused by every forward."""
+    create_block_mask), then reused by every forward.  order="lpt" issues each
+    piece's query blocks longest first; None keeps index order."""
 
-    def __init__(self, pieces, N, device=None):
+    def __init__(self, pieces, N, device=None, order="lpt"):
         self.N = N
         self.pieces = list(pieces)
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
@@ -48,16 +57,21 @@ class SplitPlan:
         self.built = []
         for p in self.pieces:
             perm_t = None
+            if p.residue and p.perm is None:
+                p = Piece(p.mask, p.BQ, p.A, residue_perm(N, p.residue), p.residue)
             if p.perm is not None:
                 perm_t = (p.perm.to(device=dev, dtype=torch.int32) if isinstance(p.perm, torch.Tensor)
                           else torch.from_numpy(np.asarray(p.perm, dtype=np.int32)).to(dev))
             mask = Permuted(p.mask, perm_t.cpu().numpy()) if perm_t is not None else p.mask
-            kv_idx, kv_num, kv_partial, wave, tiles, live = build_device(mask, N, p.BQ, p.A, device=dev)
+            kv_idx, kv_num, kv_partial, wave, tiles, live, bits = build_device(mask, N, p.BQ, p.A, device=dev,
+                                                                                bits=True)
             inc, exc = p.mask.terms()
-            order = None
+            # longest-processing-time first: query blocks with the most listed tiles are
+            # issued first, so the tail of the grid is short blocks
+            qorder = torch.argsort(kv_num, descending=True, stable=True).to(torch.int32) if order == "lpt" else None
             self.built.append(dict(piece=p, spec=MaskSpec(tuple(inc), tuple(exc)), perm=perm_t,
-                                   kv_idx=kv_idx, kv_num=kv_num, kv_partial=kv_partial, wave=wave,
-                                   tiles=tiles, live=live, order=order))
+                                   kv_idx=kv_idx, kv_num=kv_num, kv_partial=kv_partial, wave=wave, bits=bits,
+                                   tiles=tiles, live=live, order=qorder))
 
     @property
     def live(self):
@@ -67,21 +81,32 @@ class SplitPlan:
     def elements(self):
         return sum(b["tiles"] * b["piece"].BQ * b["piece"].A for b in self.built)
 
-    def forward(self, q, k, v, scale=None, out=None, lse=None):
-        """o [BH, N, D] in q's dtype; lse (float32 [BH, N]) receives the merged log-sum-exp."""
+    def prepare(self, q, k, v, scale=None, out=None, lse=None):
+        """One validated Launch per piece over these tensors; calling them in order is a forward.
+        Returns (launches, o, lse)."""
         BH, N, D = q.shape
         if N != self.N:
             raise ValueError(f"plan built for N={self.N}, got N={N}")
         o = out if out is not None else torch.empty_like(q)
         lse_buf = lse if lse is not None else torch.empty((BH, N), dtype=torch.float32, device=q.device)
+        launches = []
         for i, b in enumerate(self.built):
             p = b["piece"]
             permuted = b["perm"] is not None
-            block_sparse_attention(
+            launches.append(prepare(
                 q, k, v, b["kv_idx"], b["kv_num"], b["kv_partial"], b["spec"], 0, 0, 0, p.BQ, p.A,
                 scale=scale, perm_q=b["perm"], perm_kv=b["perm"], gather_kv=permuted,
-                kv_wave_bits=b["wave"], gather_q=permuted, scatter_o=permuted,
-                lse=lse_buf, prev=None if i == 0 else (o, lse_buf), out=o, qblock_order=b["order"])
+                kv_wave_bits=b["wave"], kv_bits=b["bits"], gather_q=permuted, scatter_o=permuted,
+                residue=_closed_form_residue(p, N),
+                lse=lse_buf, prev=None if i == 0 else (o, lse_buf), out=o, qblock_order=b["order"]))
+        return launches, o, lse_buf
+
+    def forward(self, q, k, v, scale=None, out=None, lse=None):
+        """o [BH, N, D] in q's dtype; lse (float32 [BH, N]) receives the merged log-sum-exp."""
+        launches, o, _ = self.prepare(q, k, v, scale, out, lse)
+        with torch.cuda.device(q.device):
+            for launch in launches:
+                launch()
         return o
 
 
