@@ -96,6 +96,17 @@ def cpu_baseline(wl, budget_s=12.0):
                        f"live pairs in the sample {live}")
 
 
+def _measured_traffic(workload):
+    """HBM bytes per attention launch from the committed counter summary
+    (profiles/attn_traffic_<workload>.json, FETCH_SIZE + WRITE_SIZE scaled by a plain
+    copy of known size), or None if that workload has not been measured."""
+    path = os.path.join(ROOT, "profiles", f"attn_traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
 def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     import torch
 
@@ -111,7 +122,10 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     build_ms = (time.perf_counter() - t0) * 1e3
     q, k, v = wl.inputs(0, dev)
     launches, o, lse = plan.prepare(q, k, v)
-    wall_ms, per = measure(launches, steps, warmup)
+    wall_ms, per_launch = measure(launches, steps, warmup)
+    per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
+    for i, bi in enumerate(plan.launched):
+        per[bi] = per_launch[i]
     live = plan.live
     flops_live = 4 * wl.D * live * wl.H
     flops_tile = 4 * wl.D * plan.elements * wl.H
@@ -154,6 +168,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--all", action="store_true")
     ap.add_argument("--report", default=None)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only copy a MIB-sized device buffer a few times (the known-size kernel that "
+                         "scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}). "
@@ -161,6 +178,15 @@ def main():
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if a.copy_calibration:
+        n = a.copy_calibration * (1 << 20) // 4
+        x = torch.ones(n, dtype=torch.int32, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps(dict(copy_calibration_bytes=n * 4, launches=3)))
+        return
     from polyhedral_amd import workloads
 
     if a.all:
@@ -194,7 +220,7 @@ def main():
                     pct_bf16_peak=round(100 * r["live_tflops"] / PEAK_TFLOPS["bf16"], 2),
                     pieces=r["pieces"], index_build_ms=r["index_build_ms"]),
         roofline=dict(bound="mfma", achieved=r["kernel_live_tflops"], peak=r["peak_tflops"], unit="TFLOP/s",
-                      frac=r["frac_peak"], traffic=None,
+                      frac=r["frac_peak"], traffic=_measured_traffic(r["workload"]),
                       kernel="attn_fwd_kernel (all launches of one step)",
                       algorithmic="live FLOP = 4 * D * live pairs * heads per launch"),
         cpu_baseline=r.get("cpu_baseline"),

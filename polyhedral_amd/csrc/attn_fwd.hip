@@ -30,10 +30,17 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   PA_CHECK_ARG(x->pitch == 0 || !x->kv_bits_off == !x->kv_bits,
                "pa_attn_fwd: kv_bits_off and kv_bits go together");
   PA_CHECK_ARG(x->residue_s <= 0 ||
-                   (x->residue_qlog2 >= 0 && x->residue_qlog2 < 31 &&
+                   (x->residue_qlog2 >= 4 && x->residue_qlog2 < 31 &&
                     (int64_t)x->residue_s << x->residue_qlog2 == x->N),
-               "pa_attn_fwd: residue_s=%d with N/s = 2^%d does not match N=%lld", x->residue_s,
-               x->residue_qlog2, (long long)x->N);
+               "pa_attn_fwd: residue_s=%d with N/s = 2^%d does not match N=%lld (N/s >= 16 needed)",
+               x->residue_s, x->residue_qlog2, (long long)x->N);
+  {
+    // a 16-row segment's in-head byte offsets are 32-bit in the kernel
+    const int64_t esz0 = x->dtype == PA_F32 ? 4 : 2;
+    const int64_t stride = x->residue_s > 0 ? x->residue_s : 1;
+    const int64_t rb = (x->k_sn > x->v_sn ? x->k_sn : x->v_sn) * esz0;
+    PA_CHECK_ARG(16 * stride * rb < (1ll << 31), "pa_attn_fwd: row stride too large for 32-bit offsets");
+  }
   PA_CHECK_ARG(!(x->gather_q || x->scatter_o) || x->mask.perm_q || x->residue_s > 0,
                "pa_attn_fwd: gather_q / scatter_o need mask.perm_q or residue_s");
   PA_CHECK_ARG(!x->gather_kv || x->mask.perm_kv || x->residue_s > 0,

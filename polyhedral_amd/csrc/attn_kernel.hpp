@@ -15,8 +15,11 @@
 //    live rows for BQ = 16).  K and V of 64 KV rows (4 segments of 16 rows, each
 //    segment taken from any listed tile) are staged per step into LDS, double
 //    buffered, the next step's global loads in flight while this one computes.
-//    K rows are stored with a 16-B XOR swizzle; V is stored transposed (V^T) for
-//    the bf16/f16 MFMA A operand, in the KV-slot order that matches P^T's.
+//    K and V rows are stored with padded pitches (bank-conflict free for their
+//    reads, all addresses affine); the bf16/f16 V^T operand of P.V comes from
+//    gfx950's transposed LDS read (ds_read_b64_tr_b16), in the KV-row order that
+//    matches P^T's registers.  Each thread's staging offsets are loop invariant;
+//    per step only a uniform segment base pointer changes.
 //  * Everything a step needs to know about its segments (tile row, wave codes,
 //    bitmap offset) is read with uniform (scalar) loads two steps ahead, and a
 //    residue-class permutation is evaluated in closed form, so no global load
@@ -121,11 +124,32 @@ __device__ __forceinline__ f32x4 load4_any(const char* p, int32_t dt) {
   return __builtin_convertvector(*reinterpret_cast<const bf16x4*>(p), f32x4);
 }
 
-__device__ __forceinline__ float other_half(float x) { return __shfl_xor(x, 32, 64); }
+// Lanes l and l ^ 32 hold the two halves of one query row's KV columns.
+// permlane32_swap(x, x) returns {x[l % 32], x[l % 32 + 32]} in every lane.
+__device__ __forceinline__ float row_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+__device__ __forceinline__ float row_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+  return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+}
 
-// Uniform description of the 4 segments of one step.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives element i % 4 of the
+// 8-byte reads of lanes 4e + i / 4 (e = 0..3).  If lane j of the group reads 4
+// consecutive columns c0 + 4 (j % 4) of row r0 + j / 4, lane i gets column c0 + i of
+// rows r0..r0+3: a transposed 4 x 16 tile.
+__device__ __forceinline__ s16x4 lds_read_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
+// Uniform description of the 4 segments (16 index-space KV rows each) of one step.
 struct StepMeta {
   int32_t base[4];   // index-space KV row of the segment's first row; -1 past the list
+  int32_t grow[4];   // global row of the segment's first row (after the basis change)
   uint32_t code[4];  // tile code shifted to the segment's column group (0 past the list)
   int32_t boff[4];   // bitmap word offset of the segment's tile (-1: none)
 };
@@ -138,6 +162,18 @@ constexpr int occupancy_target() {
   return (NW == 4 && (sizeof(T) == 2 || D == 64)) ? 2 : 1;
 }
 
+// LDS row pitches.  K: one extra 16-B unit, so the 16 rows a 128-bit read touches at
+// one column fall in 16 different bank groups.  V (bf16/f16): 64 extra bytes, so the
+// 4 consecutive rows of a transposed read fall in 4 disjoint 16-bank ranges.  Padding
+// instead of an XOR swizzle keeps every address affine: one base register per lane
+// plus immediate offsets.
+template <typename T, int D>
+constexpr int k_pitch() { return D * (int)sizeof(T) + 16; }
+template <typename T, int D>
+constexpr int v_pitch() { return D * (int)sizeof(T) + (sizeof(T) == 2 ? 64 : 16); }
+template <typename T, int D>
+constexpr int buf_bytes() { return kStep * (k_pitch<T, D>() + v_pitch<T, D>()); }
+
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(occupancy_target<T, D, NW>())))
 void attn_fwd_kernel(const AttnK a) {
@@ -145,12 +181,13 @@ void attn_fwd_kernel(const AttnK a) {
   constexpr int ESZ = sizeof(T);
   constexpr int UPR = D * ESZ / 16;                 // 16-B units per row
   constexpr int NT = NW * 64;
-  constexpr int K_BYTES = kStep * D * ESZ;          // K tile (and V tile) bytes per buffer
-  constexpr int BUF_BYTES = 2 * K_BYTES;
-  constexpr int KU = (kStep * UPR + NT - 1) / NT;   // K units per thread
-  constexpr int VTASKS = kF32 ? 0 : 16 * UPR;       // V^T tasks (4 rows x 16 B each)
-  constexpr int VT = kF32 ? 0 : (VTASKS + NT - 1) / NT;
-  constexpr int VU = kF32 ? KU : 1;                 // f32: V staged like K
+  constexpr int KP = k_pitch<T, D>();
+  constexpr int VP = v_pitch<T, D>();
+  constexpr int K_BYTES = kStep * KP;
+  constexpr int BUF = buf_bytes<T, D>();
+  constexpr int KU = kStep * UPR / NT;              // K (and V) 16-B units per thread
+  static_assert(kStep * UPR % NT == 0, "staging units must divide evenly over the threads");
+  constexpr int SEGU = 16 * UPR;                    // units per 16-row segment
   constexpr int NDB = D / 32;                       // 32-wide output blocks
   constexpr int ROWS = NW * 32;                     // query rows held by the work-group
   constexpr int BW = (4 * ROWS + NT - 1) / NT;      // bitmap words staged per thread
@@ -181,17 +218,22 @@ void attn_fwd_kernel(const AttnK a) {
   const bool use_bits = a.kv_bits != nullptr;
 
   // index-space position -> original position
+  const bool closed = a.residue_s != 0;
   const int32_t rmask = (1 << a.residue_qlog2) - 1;
-  auto orig_q = [&](int p) -> int {
-    if (a.residue_s) return (p & rmask) * a.residue_s + (p >> a.residue_qlog2);
+  auto orig_q = [&](int p) __attribute__((always_inline)) -> int {
+    if (closed) return (p & rmask) * a.residue_s + (p >> a.residue_qlog2);
     return a.pred.perm_q ? a.pred.perm_q[p] : p;
   };
-  auto orig_kv = [&](int p) -> int {
-    if (a.residue_s) return (p & rmask) * a.residue_s + (p >> a.residue_qlog2);
+  auto orig_kv = [&](int p) __attribute__((always_inline)) -> int {
+    if (closed) return (p & rmask) * a.residue_s + (p >> a.residue_qlog2);
     return a.pred.perm_kv ? a.pred.perm_kv[p] : p;
   };
-  const bool has_pq = a.residue_s || a.pred.perm_q;
-  const bool gather_kv = a.gather_kv && (a.residue_s || a.pred.perm_kv);
+  const bool has_pq = closed || a.pred.perm_q;
+  const bool gather_kv = a.gather_kv && (closed || a.pred.perm_kv);
+  // rows of a segment are an arithmetic progression of global rows unless a permutation
+  // table is gathered through (then every row is looked up)
+  const bool table = gather_kv && !closed;
+  const int rstride = (gather_kv && closed) ? a.residue_s : 1;
 
   const int rows_valid = a.BQ < 32 ? a.BQ : 32;
   const bool q_ok = m < rows_valid;
@@ -235,20 +277,35 @@ void attn_fwd_kernel(const AttnK a) {
 
   const char* kbase = a.k + bh * a.k_sb * ESZ;
   const char* vbase = a.v + bh * a.v_sb * ESZ;
+  const int64_t krow_b = a.k_sn * ESZ, vrow_b = a.v_sn * ESZ;  // bytes per global row
+
+  // ---- per-thread staging geometry -------------------------------------------
+  // unit i of this thread: u = i * NT + tid -> row r = i * (NT / UPR) + tid / UPR (0..63),
+  // 16-B unit tid % UPR, segment r / 16, row within the segment r % 16.
+  constexpr int RPI = NT / UPR;         // rows advanced per unit index
+  const int t_row = tid / UPR;          // row of unit 0
+  const int t_un16 = (tid % UPR) * 16;  // byte offset of this thread's unit inside a row
+  const int64_t kstep_b = (int64_t)rstride * krow_b, vstep_b = (int64_t)rstride * vrow_b;
+  // segment of unit i: compile-time when a block of NT units sits inside one segment,
+  // else one of two (NT = 2 * SEGU), picked by a fixed per-thread flag
+  const bool hi_half = NT > SEGU && (tid >= SEGU);
 
   // ---- per-step metadata (uniform, scalar loads) -----------------------------
-  auto step_meta = [&](int j) -> StepMeta {
+  auto step_meta = [&](int j) __attribute__((always_inline)) -> StepMeta {
     StepMeta mt;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int seg = 4 * j + t;
       mt.base[t] = -1;
+      mt.grow[t] = 0;
       mt.code[t] = 0u;
       mt.boff[t] = -1;
       if (seg < n_seg) {
         const int64_t ti = row0 + (seg >> spt_log2);
         const int within = seg & spt_mask;
-        mt.base[t] = a.kv_idx[ti] * A + within * 16;
+        const int b0 = a.kv_idx[ti] * A + within * 16;
+        mt.base[t] = b0;
+        mt.grow[t] = (gather_kv && closed) ? orig_kv(b0) : b0;
         if (a.kv_wave_bits) {
           const int cg = A >= 32 ? (within >> 1) : 0;
           mt.code[t] = a.kv_wave_bits[ti] >> (2 * cg);
@@ -260,146 +317,91 @@ void attn_fwd_kernel(const AttnK a) {
     }
     return mt;
   };
-  auto seg_base = [](const StepMeta& mt, int r) -> int {
-    const int t = r >> 4;
-    return t == 0 ? mt.base[0] : t == 1 ? mt.base[1] : t == 2 ? mt.base[2] : mt.base[3];
-  };
 
   // ---- staging ------------------------------------------------------------
-  uint4 kreg[KU];
-  uint4 vreg[kF32 ? VU : VT][kF32 ? 1 : 4];
-  uint32_t breg[BW];
+  // Prefetch (PA_LOAD_STEP) and LDS store (PA_STORE_STEP) are macros rather than
+  // lambdas: a lambda capturing the staging arrays by reference made the compiler keep
+  // them in scratch and wait on every prefetch load right after issuing it.
+  // Unit i of a thread belongs to segment (i * NT) / SEGU (+1 in the upper half when
+  // NT = 2 * SEGU); past-the-list rows read row 0 (valid memory) and V is zeroed there
+  // so P = 0 never meets a non-finite value (their scores are masked).
+  // The staging registers are single vector values (never memory): element 4 i + c is
+  // dword c of unit i.
+  typedef uint32_t stage_t __attribute__((ext_vector_type(4 * KU)));
+  typedef uint32_t bstage_t __attribute__((ext_vector_type(BW < 2 ? 2 : BW)));
+  stage_t kreg, vreg;
+  bstage_t breg;
 
-  auto load_row = [&](const StepMeta& mt, int r) -> int {  // global row, or -1
-    const int b0 = seg_base(mt, r);
-    if (b0 < 0) return -1;
-    const int kvr = b0 + (r & 15);
-    return gather_kv ? orig_kv(kvr) : kvr;
-  };
+#define PA_LOAD_STEP(mt) \
+  do { \
+_Pragma("unroll") \
+    for (int i = 0; i < KU; ++i) { \
+      const int t0 = (i * NT) / SEGU; \
+      const int t = (NT > SEGU) ? t0 + (hi_half ? 1 : 0) : t0; \
+      const int grow = t == 0 ? (mt).grow[0] : t == 1 ? (mt).grow[1] : t == 2 ? (mt).grow[2] : (mt).grow[3]; \
+      const int b0 = t == 0 ? (mt).base[0] : t == 1 ? (mt).base[1] : t == 2 ? (mt).base[2] : (mt).base[3]; \
+      const bool valid = b0 >= 0; \
+      const int rr = (i * RPI + t_row) & 15; \
+      uint4 kx, vx; \
+      if (!table) { \
+        const char* kp = kbase + (int64_t)grow * krow_b; \
+        const char* vp = vbase + (int64_t)grow * vrow_b; \
+        kx = *reinterpret_cast<const uint4*>(kp + (int)(rr * kstep_b) + t_un16); \
+        vx = *reinterpret_cast<const uint4*>(vp + (int)(rr * vstep_b) + t_un16); \
+      } else { \
+        const int lr = valid ? a.pred.perm_kv[b0 + rr] : 0; \
+        kx = *reinterpret_cast<const uint4*>(kbase + (int64_t)lr * krow_b + t_un16); \
+        vx = *reinterpret_cast<const uint4*>(vbase + (int64_t)lr * vrow_b + t_un16); \
+      } \
+      if (!valid) vx = uint4{0, 0, 0, 0}; \
+      kreg[4 * i] = kx.x; kreg[4 * i + 1] = kx.y; kreg[4 * i + 2] = kx.z; kreg[4 * i + 3] = kx.w; \
+      vreg[4 * i] = vx.x; vreg[4 * i + 1] = vx.y; vreg[4 * i + 2] = vx.z; vreg[4 * i + 3] = vx.w; \
+    } \
+    if (use_bits) { \
+      const int wpr = (A + 31) >> 5; \
+_Pragma("unroll") \
+      for (int i = 0; i < BW; ++i) { \
+        const int x = tid + i * NT; \
+        breg[i] = 0u; \
+        const int t = x / ROWS, rr = x % ROWS; \
+        if (x < 4 * ROWS) { \
+          const int off = t == 0 ? (mt).boff[0] : t == 1 ? (mt).boff[1] : t == 2 ? (mt).boff[2] : (mt).boff[3]; \
+          const int sb = t == 0 ? (mt).base[0] : t == 1 ? (mt).base[1] : t == 2 ? (mt).base[2] : (mt).base[3]; \
+          const int col = sb & (A - 1); \
+          if (off >= 0 && rr < a.BQ) breg[i] = a.kv_bits[(int64_t)off + rr * wpr + (col >> 5)] >> (col & 31); \
+        } \
+      } \
+    } \
+  } while (0)
 
-  auto load_step = [&](const StepMeta& mt) {
-#pragma unroll
-    for (int i = 0; i < KU; ++i) {
-      const int u = tid + i * NT;
-      kreg[i] = uint4{0, 0, 0, 0};
-      if (u < kStep * UPR) {
-        const int r = u / UPR, un = u % UPR;
-        const int lr = load_row(mt, r);
-        if (lr >= 0) kreg[i] = *reinterpret_cast<const uint4*>(kbase + ((int64_t)lr * a.k_sn) * ESZ + un * 16);
-      }
-    }
-    if constexpr (kF32) {
-#pragma unroll
-      for (int i = 0; i < VU; ++i) {
-        const int u = tid + i * NT;
-        vreg[i][0] = uint4{0, 0, 0, 0};
-        if (u < kStep * UPR) {
-          const int r = u / UPR, un = u % UPR;
-          const int lr = load_row(mt, r);
-          if (lr >= 0)
-            vreg[i][0] = *reinterpret_cast<const uint4*>(vbase + ((int64_t)lr * a.v_sn) * ESZ + un * 16);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < VT; ++i) {
-        const int t = tid + i * NT;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vreg[i][e] = uint4{0, 0, 0, 0};
-        if (t < VTASKS) {
-          const int g = t / UPR, un = t % UPR;
-          // slot group g holds rows 16*(g/4) + 4*swap(g%4) + 0..3, swap = {0, 2, 1, 3}
-          const int gg = g & 3;
-          const int rbase = 16 * (g >> 2) + 4 * (((gg & 1) << 1) | (gg >> 1));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int lr = load_row(mt, rbase + e);
-            if (lr >= 0)
-              vreg[i][e] = *reinterpret_cast<const uint4*>(vbase + ((int64_t)lr * a.v_sn) * ESZ + un * 16);
-          }
-        }
-      }
-    }
-    if (use_bits) {
-      const int wpr = (A + 31) >> 5;
-#pragma unroll
-      for (int i = 0; i < BW; ++i) {
-        const int x = tid + i * NT;
-        breg[i] = 0u;
-        if (x < 4 * ROWS) {
-          const int t = x / ROWS, rr = x % ROWS;
-          const int off = t == 0 ? mt.boff[0] : t == 1 ? mt.boff[1] : t == 2 ? mt.boff[2] : mt.boff[3];
-          const int sb = t == 0 ? mt.base[0] : t == 1 ? mt.base[1] : t == 2 ? mt.base[2] : mt.base[3];
-          const int col = sb & (A - 1);  // first column of the segment inside its tile
-          if (off >= 0 && rr < a.BQ) breg[i] = a.kv_bits[(int64_t)off + rr * wpr + (col >> 5)] >> (col & 31);
-        }
-      }
-    }
-  };
-
-  auto ksw = [](int r) -> int { return UPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
-
-  auto store_step = [&](const StepMeta& mt, int b) {
-    char* Ks = smem + b * BUF_BYTES;
-    char* Vs = Ks + K_BYTES;
-#pragma unroll
-    for (int i = 0; i < KU; ++i) {
-      const int u = tid + i * NT;
-      if (u < kStep * UPR) {
-        const int r = u / UPR, un = u % UPR;
-        *reinterpret_cast<uint4*>(Ks + (r * UPR + (un ^ ksw(r))) * 16) = kreg[i];
-      }
-    }
-    if constexpr (kF32) {
-#pragma unroll
-      for (int i = 0; i < VU; ++i) {
-        const int u = tid + i * NT;
-        if (u < kStep * UPR) {
-          const int r = u / UPR, un = u % UPR;
-          *reinterpret_cast<uint4*>(Vs + (r * UPR + (un ^ ksw(r))) * 16) = vreg[i][0];
-        }
-      }
-    } else {
-      // V^T[d][slot]: 64 slots of 2 B = 128 B per d row, 16-B unit swizzle unit ^ ((d >> 1) & 7)
-#pragma unroll
-      for (int i = 0; i < VT; ++i) {
-        const int t = tid + i * NT;
-        if (t < VTASKS) {
-          const int g = t / UPR, un = t % UPR;
-          // 16-bit element e of a 16-B unit: word e / 2, half e % 2 (no address taken,
-          // so the staging registers never go to scratch)
-          auto half = [](const uint4& u, int e) -> uint32_t {
-            const uint32_t wv = e < 2 ? u.x : e < 4 ? u.y : e < 6 ? u.z : u.w;
-            return (e & 1) ? (wv >> 16) : (wv & 0xffffu);
-          };
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int d = 8 * un + e;
-            uint2 val;
-            val.x = half(vreg[i][0], e) | (half(vreg[i][1], e) << 16);
-            val.y = half(vreg[i][2], e) | (half(vreg[i][3], e) << 16);
-            const int unit = (g >> 1) ^ ((d >> 1) & 7);
-            *reinterpret_cast<uint2*>(Vs + d * 128 + unit * 16 + (g & 1) * 8) = val;
-          }
-        }
-      }
-    }
-    if (use_bits) {
-#pragma unroll
-      for (int i = 0; i < BW; ++i) {
-        const int x = tid + i * NT;
-        if (x < 4 * ROWS) bits_s[b][x / ROWS][x % ROWS] = breg[i];
-      }
-    } else if (tid < kStep) {
-      // predicate path: original KV coordinate of every staged row
-      const int b0 = seg_base(mt, tid);
-      kvo_s[b][tid] = b0 < 0 ? -1 : orig_kv(b0 + (tid & 15));
-    }
-  };
+#define PA_STORE_STEP(mt, b) \
+  do { \
+    char* buf = smem + (b) * BUF; \
+    char* kdst = buf + t_row * KP + t_un16; \
+    char* vdst = buf + K_BYTES + t_row * VP + t_un16; \
+_Pragma("unroll") \
+    for (int i = 0; i < KU; ++i) { \
+      *reinterpret_cast<uint4*>(kdst + i * RPI * KP) = uint4{kreg[4 * i], kreg[4 * i + 1], kreg[4 * i + 2], kreg[4 * i + 3]}; \
+      *reinterpret_cast<uint4*>(vdst + i * RPI * VP) = uint4{vreg[4 * i], vreg[4 * i + 1], vreg[4 * i + 2], vreg[4 * i + 3]}; \
+    } \
+    if (use_bits) { \
+_Pragma("unroll") \
+      for (int i = 0; i < BW; ++i) { \
+        const int x = tid + i * NT; \
+        if (x < 4 * ROWS) bits_s[(b)][x / ROWS][x % ROWS] = breg[i]; \
+      } \
+    } else if (tid < kStep) { \
+      int b0 = (mt).base[3]; \
+      if (tid < 16) b0 = (mt).base[0]; \
+      else if (tid < 32) b0 = (mt).base[1]; \
+      else if (tid < 48) b0 = (mt).base[2]; \
+      kvo_s[(b)][tid] = b0 < 0 ? -1 : orig_kv(b0 + (tid & 15)); \
+    } \
+  } while (0)
 
   // 8 live bits for elements 8h..8h+7 of block lb (segment t = 2 lb + h), a segment
   // that is partial for this wave.  Element e sits at segment row 8 * (e / 4) + 4 * G + e % 4.
-  auto seg_live8 = [&](int b, int lb, int h) -> uint32_t {
+  auto seg_live8 = [&](int b, int lb, int h) __attribute__((always_inline)) -> uint32_t {
     if (use_bits) {
       const uint32_t field = q_ok ? bits_s[b][2 * lb + h][w * 32 + m] : 0u;
       return ((field >> (4 * G)) & 0xfu) | (((field >> (8 + 4 * G)) & 0xfu) << 4);
@@ -415,6 +417,15 @@ void attn_fwd_kernel(const AttnK a) {
     return bits;
   };
 
+  // ---- loop-invariant LDS read offsets ---------------------------------------
+  // QK: lane reads K row 32 lb + m, 16-B units 2 kc + G (kc = 0..D/16-1), i.e.
+  //     k_rd + lb * 32 * KP + kc * 32.
+  const int k_rd = m * KP + G * 16;
+  // PV (bf16/f16): transposed reads of V rows 32 lb + 16 c + 4 G + j / 4 (+8), columns
+  //     32 db + 16 dgrp + 4 (j % 4) (j = lane % 16): v_rd + lb * 32 VP + c * 16 VP + db * 64.
+  const int j16 = lane & 15;
+  const int v_rd = K_BYTES + (4 * G + (j16 >> 2)) * VP + (((lane >> 4) & 1) * 16 + 4 * (j16 & 3)) * ESZ;
+
   // ---- main loop ------------------------------------------------------------
 #pragma unroll
   for (int i = 0; i < PA_MAX_TERMS; ++i)  // constant indices into the argument block
@@ -422,8 +433,8 @@ void attn_fwd_kernel(const AttnK a) {
   StepMeta m_cur = step_meta(0);
   StepMeta m_nxt = step_meta(1);
   if (n_steps > 0) {
-    load_step(m_cur);
-    store_step(m_cur, 0);
+    PA_LOAD_STEP(m_cur);
+    PA_STORE_STEP(m_cur, 0);
   }
   __syncthreads();
 
@@ -432,10 +443,9 @@ void attn_fwd_kernel(const AttnK a) {
     const int b = j & 1;
     const bool more = j + 1 < n_steps;
     const StepMeta m_after = step_meta(j + 2);  // scalar loads, in flight during this step
-    if (more) load_step(m_nxt);
+    if (more) PA_LOAD_STEP(m_nxt);
 
-    const char* Ks = smem + b * BUF_BYTES;
-    const char* Vs = Ks + K_BYTES;
+    const char* buf = smem + b * BUF;
 
     f32x16 s[2];
     bool blive[2];
@@ -447,23 +457,23 @@ void attn_fwd_kernel(const AttnK a) {
       s[lb] = f32x16{0};
       if (!blive[lb]) continue;
       // S^T block: rows = 32 KV rows of this block, cols = the wave's 32 query rows
-      const int kr = 32 * lb + m;
-      const char* krow = Ks + kr * UPR * 16;
+      const char* krow = buf + k_rd + lb * 32 * KP;
       if constexpr (kF32) {
+        // f32: lane half G holds d in [G*D/2, +D/2): 16-B reads at columns G*D/2 + c
+        const char* kr2 = buf + m * KP + lb * 32 * KP + G * (D / 2) * 4;
 #pragma unroll
         for (int c = 0; c < D / 2; c += 4) {
-          const int un = (G * (D / 2) + c) >> 2;
-          const f32x4 kx = *reinterpret_cast<const f32x4*>(krow + (un ^ ksw(kr)) * 16);
+          const f32x4 kx = *reinterpret_cast<const f32x4*>(kr2 + c * 4);
           s[lb] = Mma<float>::mma(kx[0], qf[c], s[lb]);
           s[lb] = Mma<float>::mma(kx[1], qf[c + 1], s[lb]);
           s[lb] = Mma<float>::mma(kx[2], qf[c + 2], s[lb]);
           s[lb] = Mma<float>::mma(kx[3], qf[c + 3], s[lb]);
         }
+        (void)krow;
       } else {
 #pragma unroll
         for (int kc = 0; kc < D / 16; ++kc) {
-          const int un = 2 * kc + G;
-          const uint4 kx = *reinterpret_cast<const uint4*>(krow + (un ^ ksw(kr)) * 16);
+          const uint4 kx = *reinterpret_cast<const uint4*>(krow + kc * 32);
           s[lb] = Mma<T>::mma(__builtin_bit_cast(typename Mma<T>::frag, kx), qf[kc], s[lb]);
         }
       }
@@ -486,7 +496,7 @@ void attn_fwd_kernel(const AttnK a) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[lb][i]);
         }
-      mx = fmaxf(mx, other_half(mx));
+      mx = row_max(mx);
       const float m_new = fmaxf(m_run, mx * a.c);
       if (__ballot(m_new > m_run + kLazy) != 0ull) {
         const float alpha = exp2f(m_run - m_new);
@@ -511,26 +521,30 @@ void attn_fwd_kernel(const AttnK a) {
 #pragma unroll
           for (int jj = 0; jj < 16; ++jj) {
             const int vr = 32 * lb + 8 * (jj >> 2) + 4 * G + (jj & 3);
-            const char* vrow = Vs + vr * UPR * 16;
+            const char* vrow = buf + K_BYTES + vr * VP;
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
-              const int d = 32 * db + m;
-              const float vx = *reinterpret_cast<const float*>(vrow + (((d >> 2) ^ ksw(vr)) * 16) + (d & 3) * 4);
+              const float vx = *reinterpret_cast<const float*>(vrow + (32 * db + m) * 4);
               acc[db] = Mma<float>::mma(vx, p[jj], acc[db]);
             }
           }
         } else {
+          // A operand V^T[d][kv]: lane (d = l % 32, half G) needs rows 16 c + 4 G + 0..3 and
+          // 16 c + 8 + 4 G + 0..3 (the rows of its P^T values) at column d: two transposed
+          // reads, lane j of each 16-lane group reading row r0 + j / 4, columns 4 (j % 4)..+3.
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             f32x8 pv;
 #pragma unroll
             for (int e = 0; e < 8; ++e) pv[e] = p[8 * c + e];
             const typename Mma<T>::frag pf = Mma<T>::cvt(pv);
-            const int unit0 = 4 * lb + 2 * c + G;
+            const char* v1 = buf + v_rd + (32 * lb + 16 * c) * VP;
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
-              const int d = 32 * db + m;
-              const uint4 vx = *reinterpret_cast<const uint4*>(Vs + d * 128 + ((unit0 ^ ((d >> 1) & 7)) * 16));
+              const s16x4 x1 = lds_read_tr(v1 + db * 32 * ESZ);
+              const s16x4 x2 = lds_read_tr(v1 + 8 * VP + db * 32 * ESZ);
+              const uint4 vx = {__builtin_bit_cast(uint2, x1).x, __builtin_bit_cast(uint2, x1).y,
+                                __builtin_bit_cast(uint2, x2).x, __builtin_bit_cast(uint2, x2).y};
               acc[db] = Mma<T>::mma(__builtin_bit_cast(typename Mma<T>::frag, vx), pf, acc[db]);
             }
           }
@@ -538,14 +552,14 @@ void attn_fwd_kernel(const AttnK a) {
       }
     }
 
-    if (more) store_step(m_nxt, b ^ 1);
+    if (more) PA_STORE_STEP(m_nxt, b ^ 1);
     m_cur = m_nxt;
     m_nxt = m_after;
     __syncthreads();
   }
 
   // ---- epilogue -------------------------------------------------------------
-  const float l_tot = l_part + other_half(l_part);
+  const float l_tot = row_sum(l_part);
   const bool has = l_tot > 0.f;
   float lse_v = has ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
   float a_own = has ? 1.f / l_tot : 0.f;  // weight on acc
@@ -588,7 +602,10 @@ void attn_fwd_kernel(const AttnK a) {
 
 template <typename T, int D, int NW>
 constexpr int attn_smem_bytes() {
-  return 2 * 2 * kStep * D * (int)sizeof(T);
+  return 2 * buf_bytes<T, D>();
 }
 
 }  // namespace pa
+
+#undef PA_LOAD_STEP
+#undef PA_STORE_STEP

@@ -90,15 +90,23 @@ class SplitPlan:
         o = out if out is not None else torch.empty_like(q)
         lse_buf = lse if lse is not None else torch.empty((BH, N), dtype=torch.float32, device=q.device)
         launches = []
-        for i, b in enumerate(self.built):
+        self.launched = []          # index into self.built of each launch, in order
+        first = True
+        for bi_, b in enumerate(self.built):
             p = b["piece"]
+            if b["live"] == 0 and not (first and b is self.built[-1]):
+                # an empty sub-mask leaves O and LSE unchanged: no pass (the first pass of an
+                # all-empty plan still runs, to write zeros and -inf)
+                continue
             permuted = b["perm"] is not None
             launches.append(prepare(
                 q, k, v, b["kv_idx"], b["kv_num"], b["kv_partial"], b["spec"], 0, 0, 0, p.BQ, p.A,
                 scale=scale, perm_q=b["perm"], perm_kv=b["perm"], gather_kv=permuted,
                 kv_wave_bits=b["wave"], kv_bits=b["bits"], gather_q=permuted, scatter_o=permuted,
                 residue=_closed_form_residue(p, N),
-                lse=lse_buf, prev=None if i == 0 else (o, lse_buf), out=o, qblock_order=b["order"]))
+                lse=lse_buf, prev=None if first else (o, lse_buf), out=o, qblock_order=b["order"]))
+            self.launched.append(bi_)
+            first = False
         return launches, o, lse_buf
 
     def forward(self, q, k, v, scale=None, out=None, lse=None):

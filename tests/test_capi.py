@@ -1,0 +1,78 @@
+"""The C-ABI library loads on a host without a GPU and exports every entry point the
+header declares; argument checks reject bad calls before any device work."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from polyhedral_amd import _lib
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "polyattn_amd.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(pa_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = _declared()
+    assert "pa_attn_fwd" in names and "pa_index_classify" in names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures and the header disagree"
+
+
+def test_abi_version_and_error_channel():
+    lib = _lib.lib()
+    assert lib.pa_abi_version() == _lib.ABI_VERSION
+    m = _lib.PaMask()
+    m.n_include = 1
+    rc = lib.pa_index_classify(ctypes.byref(m), 1000, 48, 32, None, None, None, None)
+    assert rc == _lib.PA_E_INVALID
+    assert b"null argument" in lib.pa_last_error() or b"BQ" in lib.pa_last_error()
+    buf = (ctypes.c_int32 * 4)()
+    rc = lib.pa_index_classify(ctypes.byref(m), 1000, 48, 32, buf, buf, buf, None)
+    assert rc == _lib.PA_E_INVALID and b"BQ=48" in lib.pa_last_error()
+
+
+def test_attention_argument_checks_run_before_any_launch():
+    lib = _lib.lib()
+    a = _lib.PaAttnArgs()
+    assert lib.pa_attn_fwd(ctypes.byref(a), None) == _lib.PA_E_INVALID      # null tensors
+    buf = (ctypes.c_int64 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    a.q = a.k = a.v = a.o = a.kv_idx = a.kv_num = a.kv_partial = p
+    a.D, a.dtype, a.BH, a.N, a.BQ, a.A = 96, _lib.PA_BF16, 1, 1024, 128, 32
+    assert lib.pa_attn_fwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"D=96" in lib.pa_last_error()
+    a.D, a.N = 128, 1000
+    assert lib.pa_attn_fwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"not divisible" in lib.pa_last_error()
+    a.N, a.mask.n_include = 1024, 0
+    assert lib.pa_attn_fwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"n_include" in lib.pa_last_error()
+
+
+def test_struct_layouts_match_the_header():
+    """ctypes field offsets of pa_attn_args follow the C layout (spot checks)."""
+    off = {f[0]: getattr(_lib.PaAttnArgs, f[0]).offset for f in _lib.PaAttnArgs._fields_}
+    assert off["q"] == 0 and off["q_sb"] == 32 and off["BH"] == 96 and off["D"] == 112
+    assert off["kv_idx"] % 8 == 0 and off["mask"] % 8 == 0
+    assert ctypes.sizeof(_lib.PaMask) == 8 + 16 * _lib.MAX_TERMS + 8 * 4
+
+
+def test_product_refuses_host_tensors():
+    """No host fallback: the drop-in entry points raise on CPU tensors."""
+    import torch
+
+    from polyhedral_amd import attention, perm
+    q = torch.zeros(1, 128, 64)
+    idx = torch.zeros(1, 1, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        attention.block_sparse_attention(q, q, q, idx, torch.ones(1, dtype=torch.int32),
+                                         torch.zeros(1, 1, dtype=torch.int8), 0, 0, 0, 0, 128, 128)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        perm.apply_perm(q, torch.arange(128, dtype=torch.int32))

@@ -1,0 +1,84 @@
+"""The five benchmark workloads at full size on the GPU: sampled query rows against the
+float64 oracle (every row of the sample checked), LSE at those rows, and whole-tensor
+properties (permuted == identity basis, split == single pass)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import masks as om
+from polyhedral_amd import workloads
+from polyhedral_amd.split import SplitPlan
+from tests.util import TOL, as64
+
+pytestmark = pytest.mark.gpu
+
+ORACLE = {"window128-L1k": "window-128", "dilated8-L8k": "dilated-8", "bandlat-L16k": "band256+lat16",
+          "sinkwin-L32k": "sinks64+win1024", "prefixlat-L64k": "prefixlm-2048"}
+
+
+def _sample_rows(L, extra=()):
+    rng = np.random.default_rng(7)
+    base = {0, 1, 63, 64, 127, 128, 255, 256, 1023, 1024, L // 2, L - 129, L - 2, L - 1, *extra}
+    return np.array(sorted({r for r in base if 0 <= r < L} | set(rng.integers(0, L, 40).tolist())))
+
+
+def _check_rows(name, o, lse, q, k, v, heads, rows):
+    spec = om.NAMED[ORACLE[name]]
+    L, D = q.shape[1], q.shape[2]
+    qs = as64(q[heads][:, rows])
+    kh, vh = as64(k[heads]), as64(v[heads])
+    M = om.live(spec, rows[:, None].astype(np.int64), np.arange(L)[None, :])
+    # dense over all keys for just these rows
+    s = np.einsum("hqd,hkd->hqk", qs, kh) * D ** -0.5
+    s = np.where(M[None], s, -np.inf)
+    mx = s.max(-1, keepdims=True)
+    mx = np.where(np.isfinite(mx), mx, 0)
+    e = np.exp(s - mx)
+    den = e.sum(-1, keepdims=True)
+    want = np.where(den > 0, np.einsum("hqk,hkd->hqd", e / np.where(den > 0, den, 1), vh), 0)
+    wlse = np.where(den[..., 0] > 0, (mx + np.log(np.where(den > 0, den, 1)))[..., 0], -np.inf)
+    got = as64(o[heads][:, rows])
+    err = np.abs(got - want)
+    tmax, tmean = TOL[q.dtype]
+    assert err.max() <= tmax, f"{name}: max abs err {err.max():.3e}"
+    if tmean is not None:
+        assert err.mean() <= tmean, f"{name}: mean abs err {err.mean():.3e}"
+    gl = lse[heads][:, rows].cpu().numpy().astype(np.float64)
+    fin = np.isfinite(wlse)
+    assert np.array_equal(np.isfinite(gl), fin)
+    assert np.abs(gl[fin] - wlse[fin]).max() < (1e-4 if q.dtype == torch.float32 else 2e-2)
+    return err.max(), err.mean()
+
+
+@pytest.mark.parametrize("name", workloads.NAMES)
+def test_workload_sampled_rows(gpu, name):
+    wl = workloads.make(name)
+    q, k, v = wl.inputs(0, "cpu")
+    plan = SplitPlan(wl.pieces, wl.L, gpu)
+    lse = torch.empty(wl.H, wl.L, device=gpu)
+    o = plan.forward(q.to(gpu), k.to(gpu), v.to(gpu), lse=lse)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all()
+    rows = _sample_rows(wl.L, extra=(2047, 2048, 2049))
+    heads = [0, wl.H - 1]
+    mx, mean = _check_rows(name, o.cpu(), lse.cpu(), q, k, v, heads, rows)
+    print(f"{name}: sampled rows max abs {mx:.2e} mean abs {mean:.2e}")
+
+
+def test_dilated8_permuted_equals_identity_basis(gpu):
+    wl = workloads.make("dilated8-L8k")
+    q, k, v = (x.to(gpu) for x in wl.inputs(0, "cpu"))
+    a = SplitPlan(wl.pieces, wl.L, gpu).forward(q, k, v)
+    b = SplitPlan(wl.variants["identity"], wl.L, gpu).forward(q, k, v)
+    d = (a.float() - b.float()).abs()
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 2e-3
+
+
+def test_bandlat_split_equals_single_pass(gpu):
+    wl = workloads.make("bandlat-L16k")
+    q, k, v = (x.to(gpu) for x in wl.inputs(0, "cpu"))
+    a = SplitPlan(wl.pieces, wl.L, gpu).forward(q, k, v)
+    b = SplitPlan(wl.variants["single-rp16"], wl.L, gpu).forward(q, k, v)
+    d = (a.float() - b.float()).abs()
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 2e-3
