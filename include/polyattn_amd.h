@@ -107,6 +107,23 @@ int pa_index_bits(const pa_mask* mask, int64_t N, int32_t BQ, int32_t A, const i
                   const int32_t* kv_num, const int8_t* kv_partial, int64_t pitch,
                   const int64_t* part_base, int32_t* kv_bits_off, uint32_t* pool, void* stream);
 
+/* Step descriptors of the streaming attention kernel (no counterpart in the reference:
+ * a re-layout of the lists above).  The kernel consumes a query block's list as steps of
+ * 64 kv columns = 4 segments of 16 columns (segment s of the list is column 16 (s mod
+ * A/16) of listed tile s div (A/16)).  For query block i and step j, 16 int32 words at
+ * steps[(i * steps_pitch + j) * 16]:
+ *   [0..3]  index-space kv column of segment t's first column, -1 past the list
+ *   [4]     byte t = codes of segment t for the 4 row groups of 32 query rows:
+ *           bit 2g = some pair live, bit 2g+1 = every pair live (from kv_wave_bits, or
+ *           from kv_partial when that is NULL: 0x55 partial, 0xff full)
+ *   [5..8]  pool word offset of the bitmap word holding segment t's columns
+ *           (kv_bits_off + (16 (s mod A/16)) / 32), -1 when the tile has no bitmap
+ *   [9..15] zero
+ * steps_pitch >= ceil(pitch * A / 64).  kv_wave_bits and kv_bits_off may be NULL. */
+int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
+                   const uint32_t* kv_wave_bits, const int32_t* kv_bits_off, int64_t pitch, int64_t N,
+                   int32_t BQ, int32_t A, int32_t* steps, int64_t steps_pitch, void* stream);
+
 /* ---- class-A permutation (replaces gpu/permute.py:12-31) -------------------------
  * Row gather dst[b, p, :] = src[b, perm[p], :] (inverse = 0), the index_select of
  * gpu/permute.py:22-24, or row scatter dst[b, perm[p], :] = src[b, p, :] (inverse = 1),
@@ -157,6 +174,9 @@ typedef struct pa_attn_args {
   int64_t prev_sb, prev_sn;
   const float* prev_lse;   /* [BH, N] stride lse_sb, required with prev_o */
   const int32_t* qblock_order; /* NULL or [N/BQ] permutation: order query blocks are issued */
+  const int32_t* kv_steps;     /* NULL or pa_index_steps output for this index: enables the     */
+  int64_t steps_pitch;         /*   streaming kernel (f16/bf16, D = 128, BQ = 128, A in 16, 32, */
+                               /*   64, bitmaps for the partial tiles, no table gather of K/V)  */
 } pa_attn_args;
 
 int pa_attn_fwd(const pa_attn_args* args, void* stream);

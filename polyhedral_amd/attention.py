@@ -24,14 +24,22 @@ through perm_q and write O rows back to original positions: the class-A
 permutation fused into the kernel's loads and stores), lse (write the natural-log
 sum-exp per row), prev = (o_prev, lse_prev) (merge a partial over a disjoint
 sub-mask by log-sum-exp in the epilogue), out, qblock_order, residue (perm_q and
-perm_kv are residue_perm(N, residue): the kernel computes them in closed form).
+perm_kv are residue_perm(N, residue): the kernel computes them in closed form),
+kv_steps (step descriptors from blockindex.build_steps; found automatically for an
+index made by blockindex.build at a streaming tile shape), kernel ("auto": the
+streaming kernel whenever its preconditions hold and the index carries its arrays;
+"stream": require it; "general": the general kernel).
+
+Two HIP kernels serve the call.  The streaming kernel (f16 / bf16, D = 128, BQ = 128,
+A in 16, 32, 64) moves K and V into LDS by DMA and masks from bitmaps; the general
+kernel takes every other shape and dtype and can evaluate the predicate itself.
 """
 import ctypes
 
 import torch
 
 from . import _lib
-from .index import wave_bits_for
+from .index import STREAM_TILES, stream_arrays_for, wave_bits_for
 from .spec import DeviceMask, MaskSpec, as_perm_tensor
 
 CAUSAL, WINDOW, DILATED, LOCAL_STRIDED, TWOBAND, SINKS, PREFIX_LM = 0, 1, 2, 3, 4, 5, 6
@@ -61,8 +69,9 @@ class Launch:
     """A validated pa_attn_fwd argument block and the tensors its pointers refer to.
     __call__ launches it on the current stream of its device (no re-validation)."""
 
-    def __init__(self, args, keep, out, device):
+    def __init__(self, args, keep, out, device, kernel):
         self.args, self.keep, self.out, self.device = args, keep, out, device
+        self.kernel = kernel  # "stream" or "general"
         self._ref = ctypes.byref(args)
 
     def __call__(self):
@@ -88,8 +97,7 @@ def block_sparse_attention(q, k, v, kv_idx, kv_num, kv_partial,
 def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=None,
             perm_q=None, perm_kv=None, gather_kv=False, gather_mult=1, gather_scatter=True,
             num_warps=4, num_stages=2, *, kv_wave_bits=None, kv_bits=None, gather_q=False, scatter_o=False,
-            residue=0,
-            lse=None, prev=None, out=None, qblock_order=None):
+            residue=0, lse=None, prev=None, out=None, qblock_order=None, kv_steps=None, kernel="auto"):
     """Validate the arguments of block_sparse_attention once and return a Launch."""
     BH, N, D = q.shape
     if perm_kv is None:
@@ -119,6 +127,14 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
         kv_wave_bits = kv_wave_bits.to(torch.int32).contiguous()
         if kv_wave_bits.shape != kv_idx.shape:
             raise ValueError("kv_wave_bits must have the shape of kv_idx")
+    if kernel not in ("auto", "stream", "general"):
+        raise ValueError(f"kernel={kernel!r}: expected 'auto', 'stream' or 'general'")
+    if kernel != "general" and (kv_bits is None or kv_steps is None):
+        reg_bits, reg_steps = stream_arrays_for(kv_idx, BQ, A)
+        if kv_bits is None and kv_steps is None:
+            kv_bits = reg_bits
+        if kv_steps is None and (kv_bits is reg_bits or kv_bits is None):
+            kv_steps = reg_steps
 
     dev = q.device
     if isinstance(kind, DeviceMask):
@@ -153,7 +169,8 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
             raise ValueError("kv_bits must be (int32 offsets shaped like kv_idx, int32 bitmap pool)")
         args.kv_bits_off, args.kv_bits = _lib.ptr(bits_off), _lib.ptr(bits_pool)
     args.mask = dmask.struct()
-    args.gather_q, args.gather_kv, args.scatter_o = int(bool(gather_q)), int(bool(gather_kv)), int(bool(scatter_o))
+    gathers_kv = bool(gather_kv) and (perm_kv is not None or bool(residue))
+    args.gather_q, args.gather_kv, args.scatter_o = int(bool(gather_q)), int(gathers_kv), int(bool(scatter_o))
     if residue:
         # perm_q = perm_kv = residue_perm(N, residue), evaluated in closed form by the kernel
         qn = N // residue
@@ -184,5 +201,26 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
         if qblock_order.numel() != nq:
             raise ValueError("qblock_order must have N/BQ entries")
         args.qblock_order = _lib.ptr(qblock_order)
-    keep = [q, k, v, o, kv_idx, kv_num, kv_partial, kv_wave_bits, kv_bits, dmask, lse, prev, qblock_order]
-    return Launch(args, keep, o, dev)
+    # the streaming kernel's preconditions (pa_attn_fwd rejects kv_steps otherwise)
+    pitch = kv_idx.shape[1]
+    why = None
+    if q.dtype not in (torch.float16, torch.bfloat16) or D != 128 or (BQ, A) not in STREAM_TILES:
+        why = f"dtype {q.dtype}, D={D}, tile {BQ}x{A} (needs f16/bf16, D=128, BQ=128, A in 16/32/64)"
+    elif gathers_kv and not residue:
+        why = "K/V gathered through a permutation table (only the closed-form residue basis)"
+    elif pitch and kv_bits is None:
+        why = "no partial-tile bitmaps for this index"
+    elif pitch and kv_steps is None:
+        why = "no step descriptors for this index"
+    if kernel == "stream" and why is not None:
+        raise ValueError(f"the streaming kernel cannot take this call: {why}")
+    use_stream = kernel != "general" and why is None and pitch > 0
+    if use_stream:
+        _lib.require_device(kv_steps)
+        if kv_steps.dtype != torch.int32 or kv_steps.dim() != 3 or kv_steps.shape[0] != nq \
+                or kv_steps.shape[2] != 16 or not kv_steps.is_contiguous():
+            raise ValueError("kv_steps must be contiguous int32 [N/BQ, steps, 16]")
+        args.kv_steps, args.steps_pitch = _lib.ptr(kv_steps), kv_steps.shape[1]
+    keep = [q, k, v, o, kv_idx, kv_num, kv_partial, kv_wave_bits, kv_bits, dmask, lse, prev, qblock_order,
+            kv_steps]
+    return Launch(args, keep, o, dev, "stream" if use_stream else "general")

@@ -21,7 +21,7 @@ LIB = LIBDIR / "libpolyattn_amd.so"
 ARCH = "gfx950"
 
 SOURCES = ["common.hip", "index.hip", "permute.hip", "merge.hip", "attn_fwd.hip",
-           "attn_bf16.hip", "attn_f16.hip", "attn_f32.hip"]
+           "attn_bf16.hip", "attn_f16.hip", "attn_f32.hip", "attn_stream.hip"]
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object-version=5",
@@ -44,9 +44,14 @@ def _torch_lib():
     return pathlib.Path(spec.origin).parent / "lib"
 
 
+# per-source additions: the streaming kernel computes no NaN on purpose (masked scores
+# are -inf, never NaN), so fmax needs no NaN-quieting instructions
+EXTRA_FLAGS = {"attn_stream.hip": ["-fno-honor-nans", "-Wno-inline-asm"]}
+
+
 def _compile(src, hipcc):
     obj = BUILD / (pathlib.Path(src).stem + ".o")
-    cmd = [hipcc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "not a recognized feature" not in l)
     if r.returncode != 0:

@@ -8,6 +8,7 @@ namespace pa {
 int launch_attn_bf16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f32(const AttnK& a, int D, int NW, hipStream_t s);
+int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s);
 }  // namespace pa
 
 extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
@@ -97,11 +98,28 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   a.prev_sn = x->prev_sn;
   a.prev_lse = x->prev_lse;
   a.qblock_order = x->qblock_order;
+  a.steps = x->kv_steps;
+  a.steps_pitch = x->steps_pitch;
   PA_CHECK_ARG(a.total_wg <= 0x7fffffffll, "pa_attn_fwd: %lld work-groups exceed the grid limit",
                (long long)a.total_wg);
 
   const int NW = x->BQ >= 32 ? x->BQ / 32 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x->kv_steps) {
+    // the streaming kernel: asked for by passing the step descriptors, so its
+    // preconditions are errors rather than a silent change of kernel
+    PA_CHECK_ARG(x->dtype == PA_BF16 || x->dtype == PA_F16, "pa_attn_fwd: kv_steps needs f16 or bf16");
+    PA_CHECK_ARG(x->D == 128 && x->BQ == 128 && (x->A == 16 || x->A == 32 || x->A == 64),
+                 "pa_attn_fwd: kv_steps needs D = 128, BQ = 128, A in 16, 32, 64 (got D=%d, %dx%d)", x->D, x->BQ,
+                 x->A);
+    PA_CHECK_ARG(!x->gather_kv || x->residue_s > 0,
+                 "pa_attn_fwd: kv_steps supports gather_kv only through the closed-form residue basis");
+    PA_CHECK_ARG(x->pitch == 0 || x->kv_bits, "pa_attn_fwd: kv_steps needs the partial-tile bitmaps");
+    PA_CHECK_ARG(x->steps_pitch >= (x->pitch * x->A + 63) / 64, "pa_attn_fwd: steps_pitch=%lld < %lld",
+                 (long long)x->steps_pitch, (long long)((x->pitch * x->A + 63) / 64));
+    PA_CHECK_ARG((reinterpret_cast<uintptr_t>(x->kv_steps) & 15) == 0, "pa_attn_fwd: kv_steps not 16-byte aligned");
+    return pa::launch_attn_stream(a, x->dtype, s);
+  }
   switch (x->dtype) {
     case PA_BF16: return pa::launch_attn_bf16(a, x->D, NW, s);
     case PA_F16: return pa::launch_attn_f16(a, x->D, NW, s);

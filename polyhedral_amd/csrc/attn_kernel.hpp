@@ -74,6 +74,8 @@ struct AttnK {
   int64_t prev_sb, prev_sn;
   const float* prev_lse;
   const int32_t* qblock_order;
+  const int32_t* steps;  // step descriptors (streaming kernel only)
+  int64_t steps_pitch;
 };
 
 constexpr int kStep = 64;          // KV rows per staged step

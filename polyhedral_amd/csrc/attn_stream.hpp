@@ -1,0 +1,368 @@
+// Streaming block-sparse attention forward for gfx950: f16 / bf16, D = 128, BQ = 128.
+//
+// Same contract and numerics as attn_fwd_kernel (the replacement of the Triton
+// kernel _attn_fwd, gpu/triton_attn.py:62-182): one work-group of 4 waves per
+// (query block, batch-head), each wave owning 32 query rows, scores computed
+// transposed (S^T = K Q^T) on 32x32x16 MFMAs, online softmax with the finite
+// -1e30 sentinel, lazy rescale and the l > 0 guard.  What differs is how K and V
+// reach the MFMAs and how little work a step costs outside them:
+//
+//  * K and V rows go from global memory straight into LDS with gfx950's LDS DMA
+//    (global_load_lds_dwordx4): no staging registers, no LDS store instructions.
+//    The DMA is issued from inline assembly so that the compiler, which cannot
+//    tell which LDS stage a DMA writes, does not wait for all of them before every
+//    LDS read; the kernel waits itself (vmcnt(0) at the top of a step, then the
+//    work-group barrier), one step ahead, with two LDS stages.
+//  * A DMA instruction writes 64 consecutive 16-byte units, so rows are stored
+//    unpadded and the bank conflicts are removed by an XOR swizzle of the 16-byte
+//    units inside a 256-byte row: K unit u of row r sits at u ^ (r & 15) (the 16
+//    rows a 128-bit read touches hit 16 different bank groups), V unit u at
+//    u ^ 4 (r & 3) (the 4 rows of a transposed read hit disjoint bank groups).
+//    The lane of a DMA picks its source unit so that the LDS layout comes out
+//    swizzled; every read address is loop invariant plus an immediate offset.
+//  * What a step needs to know (segment columns, per-wave codes, bitmap offsets) is
+//    one 64-byte descriptor built with the index (pa_index_steps), read with scalar
+//    loads two steps ahead.
+//  * Partial blocks are masked from element bitmaps that the DMA also brings into
+//    LDS; row maxima use max3, row sums are dot2 products of the packed P values.
+#pragma once
+
+#include "attn_kernel.hpp"
+
+namespace pa {
+
+struct StepDesc {
+  int32_t base[4];  // index-space kv column of each 16-column segment, -1 past the list
+  uint32_t code;    // byte t: segment t's 2-bit codes for the 4 row groups
+  int32_t boff[4];  // pool word offset of the bitmap word of segment t, -1 when none
+  int32_t pad[7];
+};
+static_assert(sizeof(StepDesc) == 64, "descriptor is 16 words");
+
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+// One LDS stage: V rows (64 x 256 B), K rows (64 x 256 B), 4 bitmap slots of 128 words.
+constexpr int kStV = 0;
+constexpr int kStK = 16384;
+constexpr int kStB = 32768;
+constexpr int kStBytes = 34816;
+constexpr int kStreamSmem = 2 * kStBytes;
+
+// LDS DMA of 16 bytes per lane (lane l writes LDS[m0 + 16 l]) / 4 bytes per lane.
+__device__ __forceinline__ void dma_x4(uint32_t m0, const char* gbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+}
+__device__ __forceinline__ void dma_x1(uint32_t m0, const char* gbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+}
+__device__ __forceinline__ void dma_wait_all() { asm volatile("s_waitcnt vmcnt(0)"); }
+
+template <typename T>
+__device__ __forceinline__ float dot2_sum(uint32_t packed, float acc);
+template <>
+__device__ __forceinline__ float dot2_sum<__bf16>(uint32_t packed, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), one, acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2_sum<_Float16>(uint32_t packed, float acc) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), one, acc, false);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_stream_kernel(const AttnK a) {
+  constexpr int D = 128;
+  constexpr int ESZ = 2;
+  constexpr int NDB = D / 32;   // 32-wide output blocks
+  constexpr int NQF = D / 16;   // Q fragments (16 dims each)
+  using Frag = typename Mma<T>::frag;
+
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char_t*)smem;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = lane >> 5;
+  const int m = lane & 31;
+
+  const int64_t lid = xcd_remap(blockIdx.x, a.total_wg);
+  const int64_t bh = lid / a.nq;
+  const int qb_lin = (int)(lid % a.nq);
+  const int qb = a.qblock_order ? a.qblock_order[qb_lin] : qb_lin;
+  const int A = a.A;
+  const int n_steps = (a.kv_num[qb] * A + 63) >> 6;
+  const StepDesc* desc = reinterpret_cast<const StepDesc*>(a.steps) + (int64_t)qb * a.steps_pitch;
+
+  const bool closed = a.residue_s != 0;
+  const int32_t rmask = (1 << a.residue_qlog2) - 1;
+  const bool has_pq = closed || a.pred.perm_q;
+  const bool gather_kv = a.gather_kv && closed;
+  const int rstride = gather_kv ? a.residue_s : 1;
+
+  const int r_idx = qb * 128 + w * 32 + m;  // index-space query row of this lane
+  int q_orig = r_idx;
+  if (has_pq) q_orig = closed ? (r_idx & rmask) * a.residue_s + (r_idx >> a.residue_qlog2) : a.pred.perm_q[r_idx];
+  const int r_load = (a.gather_q && has_pq) ? q_orig : r_idx;
+
+  const char* kbase = a.k + bh * a.k_sb * ESZ;
+  const char* vbase = a.v + bh * a.v_sb * ESZ;
+  // row offsets inside a head fit in 32 bits (checked on the host)
+  const uint32_t krow_b32 = (uint32_t)(a.k_sn * ESZ), vrow_b32 = (uint32_t)(a.v_sn * ESZ);
+  const char* bits = reinterpret_cast<const char*>(a.kv_bits);
+  const int wpr = (A + 31) >> 5;
+
+  // ---- DMA geometry (loop invariant) ----------------------------------------
+  // Wave w moves rows 4 w .. 4 w + 3 of every 16-row segment, one row per 16 lanes:
+  // lane l writes LDS unit p = l % 16 of row rs = 4 w + l / 16 and fetches the global
+  // unit that the swizzle stores there.
+  const int rs = 4 * w + (lane >> 4);
+  const int pu = lane & 15;
+  const uint32_t k_goff = (uint32_t)(rs * rstride) * krow_b32 + 16u * (uint32_t)(pu ^ rs);
+  const uint32_t v_goff = (uint32_t)(rs * rstride) * vrow_b32 + 16u * (uint32_t)(pu ^ (4 * (rs & 3)));
+  // bitmaps: A >= 32 -> wave w moves rows 64 (w & 1) + lane of block (w >> 1)'s word
+  // column; A = 16 -> wave w moves all 128 rows of segment w's word column
+  const uint32_t b_goff = A >= 32 ? (uint32_t)((64 * (w & 1) + lane) * wpr * 4) : (uint32_t)(lane * 4);
+
+  // ---- LDS read geometry (loop invariant; stage / block / row offsets are immediates)
+  // QK: lane (m, G) reads K row 32 lb + m, unit 2 kc + G.
+  // (pointers, not integer offsets: inbounds pointer arithmetic lets the stage, block
+  // and row constants fold into the instructions' offset fields)
+  const char* kptr[NQF];
+#pragma unroll
+  for (int kc = 0; kc < NQF; ++kc) kptr[kc] = smem + kStK + m * 256 + 16 * ((2 * kc + G) ^ (m & 15));
+  // PV: transposed reads of V rows 32 lb + 16 c + 4 G + j16 / 4 (+8), columns
+  // 32 db + 16 h16 + 4 (j16 % 4) .. +3; row % 4 = j16 / 4 fixes the swizzle.
+  const int j16 = lane & 15;
+  const int h16 = (lane >> 4) & 1;
+  const char* vptr[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+    vptr[db] = smem + kStV + (4 * G + (j16 >> 2)) * 256 +
+               16 * ((4 * db + 2 * h16 + ((j16 & 3) >> 1)) ^ (4 * (j16 >> 2))) + 8 * (j16 & 1);
+  const char* bptr = smem + kStB + (w * 32 + m) * 4;  // this lane's word in bitmap slot 0
+
+  // ---- Q fragments (B operand of S^T = K Q^T) --------------------------------
+  Frag qf[NQF];
+  {
+    const char* qrow = a.q + (bh * a.q_sb + (int64_t)r_load * a.q_sn) * ESZ;
+#pragma unroll
+    for (int kc = 0; kc < NQF; ++kc)
+      qf[kc] = __builtin_bit_cast(Frag, *reinterpret_cast<const uint4*>(qrow + (16 * kc + 8 * G) * ESZ));
+  }
+
+  // The compiler counts its own vector loads in vmcnt and would place the waits for Q
+  // at the first use, inside the loop, where they would also wait for the DMA of the
+  // next step; using the fragments here makes it wait once, before the loop.
+#pragma unroll
+  for (int kc = 0; kc < NQF; ++kc) asm volatile("" ::"v"(qf[kc]));
+
+  f32x16 acc[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) acc[i] = f32x16{0};
+  float m_run = kSentinel;
+  float l_part = 0.f;
+  const float cexp = a.c;
+
+  // Descriptors are read through the constant address space: the kernel never writes
+  // them, and that lets the compiler use scalar loads (a vector load would be counted
+  // in vmcnt together with the DMA and make the compiler's waits cover it).
+  auto load_desc = [&](int jd) __attribute__((always_inline)) -> StepDesc {
+    typedef const __attribute__((address_space(4))) int32_t cint;
+    cint* c = (cint*)(reinterpret_cast<const int32_t*>(desc + jd));
+    StepDesc r{};
+    r.base[0] = c[0];
+    r.base[1] = c[1];
+    r.base[2] = c[2];
+    r.base[3] = c[3];
+    r.code = (uint32_t)c[4];
+    r.boff[0] = c[5];
+    r.boff[1] = c[6];
+    r.boff[2] = c[7];
+    r.boff[3] = c[8];
+    return r;
+  };
+  StepDesc d_cur{}, d_nxt{};
+  if (n_steps > 0) d_cur = load_desc(0);
+  if (n_steps > 1) d_nxt = load_desc(1);
+
+  // Issue the DMA of step descriptor `dd` into stage SB.  A past-the-list segment loads
+  // row 0 (valid memory); its code is 0, so no wave reads its K scores unmasked or
+  // multiplies its V rows (a P.V chunk of a segment dead for the wave is skipped).
+#define PA_ISSUE(dd, SB)                                                                          \
+  do {                                                                                            \
+    _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                               \
+      const int b0 = (dd).base[t];                                                                \
+      const int g = b0 < 0 ? 0 : gather_kv ? (b0 & rmask) * a.residue_s + (b0 >> a.residue_qlog2) : b0; \
+      const uint32_t rowoff = (uint32_t)((SB) * kStBytes + (16 * t + 4 * w) * 256);               \
+      dma_x4(lds0 + rowoff + kStK, kbase + (uint32_t)g * krow_b32, k_goff);                       \
+      dma_x4(lds0 + rowoff + kStV, vbase + (uint32_t)g * vrow_b32, v_goff);                       \
+    }                                                                                             \
+    if (A >= 32) {                                                                                \
+      const int lbw = w >> 1;                                                                     \
+      const int off = lbw == 0 ? (dd).boff[0] : (dd).boff[2];                                     \
+      if (off >= 0)                                                                               \
+        dma_x1(lds0 + (SB) * kStBytes + kStB + lbw * 1024 + (w & 1) * 256, bits + (int64_t)off * 4, \
+               b_goff);                                                                           \
+    } else {                                                                                      \
+      const int off = w == 0 ? (dd).boff[0] : w == 1 ? (dd).boff[1] : w == 2 ? (dd).boff[2] : (dd).boff[3]; \
+      if (off >= 0) {                                                                             \
+        dma_x1(lds0 + (SB) * kStBytes + kStB + w * 512, bits + (int64_t)off * 4, b_goff);         \
+        dma_x1(lds0 + (SB) * kStBytes + kStB + w * 512 + 256, bits + (int64_t)off * 4, b_goff + 256); \
+      }                                                                                           \
+    }                                                                                             \
+  } while (0)
+
+  // One step on stage SB with descriptor dd: QK, mask, softmax, PV.
+#define PA_COMPUTE(dd, SB)                                                                        \
+  do {                                                                                            \
+    f32x16 s[2];                                                                                  \
+    bool blive[2], slive[4];                                                                      \
+    _Pragma("unroll") for (int lb = 0; lb < 2; ++lb) {                                            \
+      const uint32_t c0 = ((dd).code >> (16 * lb + 2 * w)) & 3u;                                  \
+      const uint32_t c1 = ((dd).code >> (16 * lb + 8 + 2 * w)) & 3u;                              \
+      const bool any0 = c0 & 1u, any1 = c1 & 1u, all0 = c0 >> 1, all1 = c1 >> 1;                  \
+      slive[2 * lb] = any0;                                                                       \
+      slive[2 * lb + 1] = any1;                                                                   \
+      blive[lb] = any0 || any1;                                                                   \
+      if (!blive[lb]) continue;                                                                   \
+      s[lb] = Mma<T>::mma(__builtin_bit_cast(Frag, *reinterpret_cast<const uint4*>(kptr[0] + (SB) * kStBytes + lb * 8192)), \
+                          qf[0], f32x16{0});                                                      \
+      _Pragma("unroll") for (int kc = 1; kc < NQF; ++kc) {                                        \
+        const uint4 kx = *reinterpret_cast<const uint4*>(kptr[kc] + (SB) * kStBytes + lb * 8192); \
+        s[lb] = Mma<T>::mma(__builtin_bit_cast(Frag, kx), qf[kc], s[lb]);                          \
+      }                                                                                           \
+      if (!(all0 && all1)) {                                                                      \
+        uint32_t word;                                                                            \
+        if (A >= 32) {                                                                            \
+          word = *reinterpret_cast<const uint32_t*>(bptr + (SB) * kStBytes + lb * 1024);                \
+        } else {                                                                                  \
+          const uint32_t lo = all0 ? 0xffffu                                                      \
+                                   : any0 ? *reinterpret_cast<const uint32_t*>(bptr + (SB) * kStBytes + (2 * lb) * 512) & 0xffffu \
+                                          : 0u;                                                   \
+          const uint32_t hi = all1 ? 0xffffu                                                      \
+                                   : any1 ? *reinterpret_cast<const uint32_t*>(bptr + (SB) * kStBytes + (2 * lb + 1) * 512) & 0xffffu \
+                                          : 0u;                                                   \
+          word = lo | (hi << 16);                                                                 \
+        }                                                                                         \
+        word >>= 4 * G;                                                                           \
+        _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                          \
+          /* (a scalar copy: bit-casting the vector element itself reads element 0) */           \
+          const float sv = s[lb][i];                                                              \
+          const int32_t keep = __builtin_amdgcn_sbfe((int32_t)word, 8 * (i >> 2) + (i & 3), 1);   \
+          s[lb][i] = __builtin_bit_cast(float, (__builtin_bit_cast(int32_t, sv) & keep) |         \
+                                                   (int32_t)(0xff800000u & ~(uint32_t)keep));     \
+        }                                                                                         \
+      }                                                                                           \
+    }                                                                                             \
+    if (blive[0] || blive[1]) {                                                                   \
+      float mx = -INFINITY;                                                                       \
+      _Pragma("unroll") for (int lb = 0; lb < 2; ++lb) if (blive[lb]) {                           \
+        _Pragma("unroll") for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s[lb][i], s[lb][i + 1])); \
+      }                                                                                           \
+      mx = row_max(mx);                                                                           \
+      const float m_new = fmaxf(m_run, mx * cexp);                                                \
+      if (__ballot(m_new > m_run + kLazy) != 0ull) {                                              \
+        const float alpha = exp2f(m_run - m_new);                                                 \
+        m_run = m_new;                                                                            \
+        l_part *= alpha;                                                                          \
+        _Pragma("unroll") for (int i = 0; i < NDB; ++i) acc[i] *= alpha;                          \
+      }                                                                                           \
+      const float neg_m = -m_run;                                                                 \
+      _Pragma("unroll") for (int lb = 0; lb < 2; ++lb) {                                          \
+        if (!blive[lb]) continue;                                                                 \
+        _Pragma("unroll") for (int c = 0; c < 2; ++c) {                                           \
+          if (!slive[2 * lb + c]) continue;                                                       \
+          f32x8 pv;                                                                               \
+          _Pragma("unroll") for (int e = 0; e < 8; ++e)                                           \
+            pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[lb][8 * c + e], cexp, neg_m));         \
+          const Frag pf = Mma<T>::cvt(pv);                                                        \
+          const uint4 pw = __builtin_bit_cast(uint4, pf);                                         \
+          l_part = dot2_sum<T>(pw.x, l_part);                                                     \
+          l_part = dot2_sum<T>(pw.y, l_part);                                                     \
+          l_part = dot2_sum<T>(pw.z, l_part);                                                     \
+          l_part = dot2_sum<T>(pw.w, l_part);                                                     \
+          _Pragma("unroll") for (int db = 0; db < NDB; ++db) {                                    \
+            const char* v1 = vptr[db] + (SB) * kStBytes + (32 * lb + 16 * c) * 256;               \
+            const s16x4 x1 = lds_read_tr(v1);                                                     \
+            const s16x4 x2 = lds_read_tr(v1 + 8 * 256);                                           \
+            const uint4 vx = {__builtin_bit_cast(uint2, x1).x, __builtin_bit_cast(uint2, x1).y,  \
+                              __builtin_bit_cast(uint2, x2).x, __builtin_bit_cast(uint2, x2).y};  \
+            acc[db] = Mma<T>::mma(__builtin_bit_cast(Frag, vx), pf, acc[db]);                      \
+          }                                                                                       \
+        }                                                                                         \
+      }                                                                                           \
+    }                                                                                             \
+  } while (0)
+
+  // One step jj on stage SB: wait for this step's data, start the next step's DMA into
+  // the other stage (free: every wave has passed the barrier, so finished step jj - 1),
+  // fetch the descriptor two steps ahead, compute.
+#define PA_STEP(jj, SB)                                                                           \
+  do {                                                                                            \
+    dma_wait_all();                                                                               \
+    __syncthreads();                                                                              \
+    if ((jj) + 1 < n_steps) PA_ISSUE(d_nxt, (SB) ^ 1);                                            \
+    StepDesc d_aft{};                                                                             \
+    if ((jj) + 2 < n_steps) d_aft = load_desc((jj) + 2);                                          \
+    PA_COMPUTE(d_cur, SB);                                                                        \
+    d_cur = d_nxt;                                                                                \
+    d_nxt = d_aft;                                                                                \
+  } while (0)
+
+  if (n_steps > 0) PA_ISSUE(d_cur, 0);
+  for (int j = 0; j < n_steps; j += 2) {
+    PA_STEP(j, 0);
+    if (j + 1 >= n_steps) break;
+    PA_STEP(j + 1, 1);
+  }
+
+#undef PA_STEP
+#undef PA_COMPUTE
+#undef PA_ISSUE
+
+  // ---- epilogue (as attn_fwd_kernel) -------------------------------------------
+  const float l_tot = row_sum(l_part);
+  const bool has = l_tot > 0.f;
+  float lse_v = has ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+  float a_own = has ? 1.f / l_tot : 0.f;
+  float a_prev = 0.f;
+  const int srow = (a.scatter_o && has_pq) ? q_orig : r_idx;
+  if (a.prev_o) {
+    const float lp = a.prev_lse[bh * a.lse_sb + srow];
+    const float M = fmaxf(lse_v, lp);
+    if (M == -INFINITY) {
+      a_own = 0.f;
+      a_prev = 0.f;
+      lse_v = -INFINITY;
+    } else {
+      const float w1 = has ? expf(lse_v - M) : 0.f;
+      const float w2 = lp == -INFINITY ? 0.f : expf(lp - M);
+      const float den = w1 + w2;
+      a_own = has ? (w1 / den) / l_tot : 0.f;
+      a_prev = w2 / den;
+      lse_v = M + logf(den);
+    }
+  }
+  char* orow = a.o + (bh * a.o_sb + (int64_t)srow * a.o_sn) * ESZ;
+  const int psz = a.prev_dtype == PA_F32 ? 4 : 2;
+  const char* prow = a.prev_o ? a.prev_o + (bh * a.prev_sb + (int64_t)srow * a.prev_sn) * psz : nullptr;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int d0 = 32 * db + 8 * i4 + 4 * G;
+      f32x4 x = {acc[db][4 * i4], acc[db][4 * i4 + 1], acc[db][4 * i4 + 2], acc[db][4 * i4 + 3]};
+      x *= a_own;
+      if (prow && a_prev != 0.f) x += a_prev * load4_any(prow + d0 * psz, a.prev_dtype);
+      Mma<T>::store4(orow + d0 * ESZ, x);
+    }
+  }
+  if (a.lse && G == 0) a.lse[bh * a.lse_sb + srow] = lse_v;
+}
+
+}  // namespace pa

@@ -281,3 +281,84 @@ extern "C" int pa_index_bits(const pa_mask* mask, int64_t N, int32_t BQ, int32_t
   PA_LAUNCH_CHECK("bits_kernel");
   return PA_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Step descriptors of the streaming attention kernel: one thread per (query block,
+// step of 64 kv columns), 64 bytes out, written as four 16-byte stores.
+namespace pa {
+namespace {
+
+__global__ __launch_bounds__(kThreads) void steps_kernel(const int32_t* __restrict__ kv_idx,
+                                                          const int32_t* __restrict__ kv_num,
+                                                          const int8_t* __restrict__ kv_partial,
+                                                          const uint32_t* __restrict__ kv_wave_bits,
+                                                          const int32_t* __restrict__ kv_bits_off, int64_t pitch,
+                                                          int32_t nq, int32_t BQ, int32_t A,
+                                                          int32_t* __restrict__ steps, int64_t steps_pitch) {
+  const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (gid >= (int64_t)nq * steps_pitch) return;
+  const int qb = (int)(gid / steps_pitch);
+  const int j = (int)(gid % steps_pitch);
+  const int spt = A >> 4;                    // 16-column segments per tile
+  const int n_seg = kv_num[qb] * spt;
+  const int ncg = A >= 32 ? A >> 5 : 1;      // 32-column groups per tile
+  const int ngr = BQ >= 32 ? BQ >> 5 : 1;    // 32-row groups per query block
+  int32_t d[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) d[i] = 0;
+  uint32_t code = 0u;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int seg = 4 * j + t;
+    int32_t base = -1, boff = -1;
+    uint32_t c8 = 0u;
+    if (seg < n_seg) {
+      const int64_t ti = (int64_t)qb * pitch + seg / spt;
+      const int within = seg % spt;
+      base = kv_idx[ti] * A + within * 16;
+      if (kv_wave_bits) {
+        const int cg = A >= 32 ? within >> 1 : 0;
+        const uint32_t wb = kv_wave_bits[ti];
+        for (int g = 0; g < ngr && g < 4; ++g) c8 |= ((wb >> (2 * (g * ncg + cg))) & 3u) << (2 * g);
+      } else {
+        c8 = kv_partial[ti] ? 0x55u : 0xffu;
+      }
+      if (kv_bits_off && kv_bits_off[ti] >= 0) boff = kv_bits_off[ti] + ((within * 16) >> 5);
+    }
+    d[t] = base;
+    d[5 + t] = boff;
+    code |= c8 << (8 * t);
+  }
+  d[4] = (int32_t)code;
+  int4* dst = reinterpret_cast<int4*>(steps + gid * 16);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[i] = int4{d[4 * i], d[4 * i + 1], d[4 * i + 2], d[4 * i + 3]};
+}
+
+}  // namespace
+}  // namespace pa
+
+extern "C" int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
+                              const uint32_t* kv_wave_bits, const int32_t* kv_bits_off, int64_t pitch, int64_t N,
+                              int32_t BQ, int32_t A, int32_t* steps, int64_t steps_pitch, void* stream) {
+  PA_CHECK_ARG(kv_num, "pa_index_steps: null kv_num");
+  PA_CHECK_ARG(N >= 1 && N <= (1ll << 30), "pa_index_steps: N=%lld out of range", (long long)N);
+  PA_CHECK_ARG(pa::tile_ok(BQ) && pa::tile_ok(A) && N % BQ == 0 && N % A == 0,
+               "pa_index_steps: bad tile shape BQ=%d A=%d for N=%lld", BQ, A, (long long)N);
+  PA_CHECK_ARG(pitch >= 0, "pa_index_steps: negative pitch");
+  PA_CHECK_ARG(steps_pitch >= (pitch * A + 63) / 64,
+               "pa_index_steps: steps_pitch=%lld < ceil(pitch * A / 64) = %lld", (long long)steps_pitch,
+               (long long)((pitch * A + 63) / 64));
+  const int64_t nq = N / BQ;
+  const int64_t total = nq * steps_pitch;
+  if (total == 0) return PA_OK;
+  PA_CHECK_ARG(steps, "pa_index_steps: null steps");
+  PA_CHECK_ARG(pitch == 0 || (kv_idx && kv_partial), "pa_index_steps: null list");
+  PA_CHECK_ARG((reinterpret_cast<uintptr_t>(steps) & 15) == 0, "pa_index_steps: steps must be 16-byte aligned");
+  PA_CHECK_ARG(total / pa::kThreads < 0x7fffffffll, "pa_index_steps: too many steps");
+  hipLaunchKernelGGL(pa::steps_kernel, dim3((unsigned)((total + pa::kThreads - 1) / pa::kThreads)),
+                     dim3(pa::kThreads), 0, static_cast<hipStream_t>(stream), kv_idx, kv_num, kv_partial,
+                     kv_wave_bits, kv_bits_off, pitch, (int32_t)nq, BQ, A, steps, steps_pitch);
+  PA_LAUNCH_CHECK("steps_kernel");
+  return PA_OK;
+}

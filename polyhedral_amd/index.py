@@ -12,7 +12,10 @@ dataclass contract.
 Extensions (keyword-only): ``perm`` / ``perm_kv`` build the index of a class-A
 relabelled mask without materialising M[perm][:, perm]; ``kv_wave_bits`` is the
 per-tile code of 2 bits per 32-row x 32-column wave group (some live / all live),
-which the attention kernel uses to skip or mask at wave granularity.
+which the attention kernel uses to skip or mask at wave granularity.  For the tile
+shapes the streaming attention kernel takes (STREAM_TILES), build() also makes the
+partial-tile bitmaps (pa_index_bits) and the step descriptors (pa_index_steps) and
+keeps them with the index, so block_sparse_attention finds them from kv_idx alone.
 """
 import ctypes
 import weakref
@@ -25,16 +28,46 @@ import torch
 from . import _lib
 from .spec import device_mask
 
-# id(kv_idx device tensor) -> (weakref to it, kv_wave_bits tensor, BQ, A), so the
-# reference call surface (which passes only kv_idx / kv_num / kv_partial) still gets
-# per-wave skipping.  Keyed by id because tensors compare elementwise.
-_WAVE_BITS = {}
+# (BQ, A) tile shapes of the streaming attention kernel (f16 / bf16, D = 128)
+STREAM_TILES = ((128, 16), (128, 32), (128, 64))
+
+# id(kv_idx device tensor) -> (weakref to it, dict of the arrays made with it: wave
+# codes, bitmaps, step descriptors, and its BQ, A), so the reference call surface
+# (which passes only kv_idx / kv_num / kv_partial) still gets per-wave skipping and
+# the streaming kernel.  Keyed by id because tensors compare elementwise.
+_EXTRAS = {}
 
 
-def _register_wave_bits(kv_idx, wave, BQ, A):
+def _register(kv_idx, BQ, A, **arrays):
     key = id(kv_idx)
-    _WAVE_BITS[key] = (weakref.ref(kv_idx), wave, BQ, A)
-    weakref.finalize(kv_idx, _WAVE_BITS.pop, key, None)
+    entry = _EXTRAS.get(key)
+    if entry is None or entry[0]() is not kv_idx:
+        entry = (weakref.ref(kv_idx), dict(BQ=BQ, A=A))
+        _EXTRAS[key] = entry
+        weakref.finalize(kv_idx, _EXTRAS.pop, key, None)
+    entry[1].update(arrays)
+
+
+def _extras(kv_idx, BQ, A):
+    entry = _EXTRAS.get(id(kv_idx))
+    if entry is None or entry[0]() is not kv_idx or (entry[1]["BQ"], entry[1]["A"]) != (BQ, A):
+        return {}
+    return entry[1]
+
+
+def build_steps(kv_idx, kv_num, kv_partial, wave, bits_off, N, BQ, A):
+    """Step descriptors [N/BQ, ceil(pitch * A / 64), 16] int32 (pa_index_steps), or None
+    for an index whose every list is empty."""
+    nq, pitch = kv_idx.shape
+    sp = (pitch * A + 63) // 64
+    if sp == 0:
+        return None
+    steps = torch.empty((nq, sp, 16), dtype=torch.int32, device=kv_idx.device)
+    with torch.cuda.device(kv_idx.device):
+        _lib.check(_lib.lib().pa_index_steps(_lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial),
+                                             _lib.ptr(wave), _lib.ptr(bits_off), pitch, N, BQ, A,
+                                             _lib.ptr(steps), sp, _lib.stream_of(steps)), "pa_index_steps")
+    return steps
 
 
 @dataclass
@@ -71,12 +104,15 @@ def _default_device(device):
     return torch.device(device)
 
 
-def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None, bits=False):
+def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None, bits=False, steps=False):
     """Build on the GPU; returns (kv_idx, kv_num, kv_partial, kv_wave_bits, tiles, live) with
     device tensors and host ints.  One synchronisation (to size the padded lists).
 
     bits=True appends (kv_bits_off, kv_bits): element bitmaps of the partial tiles
-    (pa_index_bits), so the attention kernel masks by table lookup."""
+    (pa_index_bits), so the attention kernel masks by table lookup.  steps=True (which
+    implies bits) appends the step descriptors of the streaming kernel (None when every
+    list is empty)."""
+    bits = bits or steps
     assert N % BQ == 0 and N % A == 0
     dev = _default_device(device)
     dm = device_mask(mask, N, dev, perm=perm, perm_kv=perm_kv)
@@ -109,14 +145,20 @@ def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None, bits=F
                                        _lib.ptr(kv_partial), max_kv, _lib.ptr(part_base), _lib.ptr(off),
                                        _lib.ptr(pool), stream), "pa_index_bits")
             out = out + ((off, pool),)
-    _register_wave_bits(kv_idx, wave, BQ, A)
+            _register(kv_idx, BQ, A, bits=(off, pool))
+        if steps:
+            st = build_steps(kv_idx, kv_num, kv_partial, wave, out[6][0], N, BQ, A)
+            out = out + (st,)
+            _register(kv_idx, BQ, A, steps=st)
+    _register(kv_idx, BQ, A, wave=wave)
     return out
 
 
 def build(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None):
     """gpu/blockindex.py:32 build(mask, N, BQ, A), computed on the GPU."""
-    kv_idx, kv_num, kv_partial, wave, tiles, live = build_device(mask, N, BQ, A, perm=perm,
-                                                                 perm_kv=perm_kv, device=device)
+    stream = (BQ, A) in STREAM_TILES
+    kv_idx, kv_num, kv_partial, wave, tiles, live = build_device(mask, N, BQ, A, perm=perm, perm_kv=perm_kv,
+                                                                 device=device, steps=stream)[:6]
     return BlockIndex(BQ, A, N, kv_idx.cpu().numpy(), kv_num.cpu().numpy(), kv_partial.cpu().numpy(),
                       tiles * BQ * A, live, wave.cpu().numpy().view(np.uint32),
                       _device=(kv_idx, kv_num, kv_partial, wave))
@@ -134,14 +176,17 @@ def to_cuda(bi, device="cuda"):
            torch.from_numpy(np.ascontiguousarray(bi.kv_partial)).to(dev))
     if bi.kv_wave_bits is not None and dev.type == "cuda":
         wave = torch.from_numpy(np.ascontiguousarray(bi.kv_wave_bits).view(np.int32)).to(dev)
-        _register_wave_bits(kv_idx, wave, bi.BQ, bi.A)
+        _register(kv_idx, bi.BQ, bi.A, wave=wave)
     return out
 
 
 def wave_bits_for(kv_idx, BQ, A):
     """The wave-group codes registered for this kv_idx tensor at this tile shape, or None."""
-    entry = _WAVE_BITS.get(id(kv_idx))
-    if entry is None or entry[0]() is not kv_idx:
-        return None
-    _, wave, bq, a = entry
-    return wave if (bq, a) == (BQ, A) and wave.shape == kv_idx.shape else None
+    wave = _extras(kv_idx, BQ, A).get("wave")
+    return wave if wave is not None and wave.shape == kv_idx.shape else None
+
+
+def stream_arrays_for(kv_idx, BQ, A):
+    """(bitmaps, step descriptors) registered for this kv_idx tensor, or (None, None)."""
+    ex = _extras(kv_idx, BQ, A)
+    return ex.get("bits"), ex.get("steps")

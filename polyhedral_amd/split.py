@@ -23,7 +23,7 @@ import torch
 
 from . import _lib
 from .attention import prepare
-from .index import build_device
+from .index import STREAM_TILES, build_device
 from .perm import residue_perm
 from .polyattn.masks import Permuted
 from .spec import MaskSpec
@@ -49,8 +49,9 @@ class SplitPlan:
     create_block_mask), then reused by every forward.  order="lpt" issues each
     piece's query blocks longest first; None keeps index order."""
 
-    def __init__(self, pieces, N, device=None, order="lpt"):
+    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto"):
         self.N = N
+        self.kernel = kernel
         self.pieces = list(pieces)
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self.device = dev
@@ -63,14 +64,17 @@ class SplitPlan:
                 perm_t = (p.perm.to(device=dev, dtype=torch.int32) if isinstance(p.perm, torch.Tensor)
                           else torch.from_numpy(np.asarray(p.perm, dtype=np.int32)).to(dev))
             mask = Permuted(p.mask, perm_t.cpu().numpy()) if perm_t is not None else p.mask
-            kv_idx, kv_num, kv_partial, wave, tiles, live, bits = build_device(mask, N, p.BQ, p.A, device=dev,
-                                                                                bits=True)
+            stream = (p.BQ, p.A) in STREAM_TILES
+            built = build_device(mask, N, p.BQ, p.A, device=dev, bits=True, steps=stream)
+            kv_idx, kv_num, kv_partial, wave, tiles, live, bits = built[:7]
+            steps = built[7] if stream else None
             inc, exc = p.mask.terms()
             # longest-processing-time first: query blocks with the most listed tiles are
             # issued first, so the tail of the grid is short blocks
             qorder = torch.argsort(kv_num, descending=True, stable=True).to(torch.int32) if order == "lpt" else None
             self.built.append(dict(piece=p, spec=MaskSpec(tuple(inc), tuple(exc)), perm=perm_t,
                                    kv_idx=kv_idx, kv_num=kv_num, kv_partial=kv_partial, wave=wave, bits=bits,
+                                   steps=steps,
                                    tiles=tiles, live=live, order=qorder))
 
     @property
@@ -104,7 +108,8 @@ class SplitPlan:
                 scale=scale, perm_q=b["perm"], perm_kv=b["perm"], gather_kv=permuted,
                 kv_wave_bits=b["wave"], kv_bits=b["bits"], gather_q=permuted, scatter_o=permuted,
                 residue=_closed_form_residue(p, N),
-                lse=lse_buf, prev=None if first else (o, lse_buf), out=o, qblock_order=b["order"]))
+                lse=lse_buf, prev=None if first else (o, lse_buf), out=o, qblock_order=b["order"],
+                kv_steps=b["steps"], kernel=self.kernel))
             self.launched.append(bi_)
             first = False
         return launches, o, lse_buf

@@ -76,3 +76,32 @@ def test_product_refuses_host_tensors():
                                          torch.zeros(1, 1, dtype=torch.int8), 0, 0, 0, 0, 128, 128)
     with pytest.raises(RuntimeError, match="GPU only"):
         perm.apply_perm(q, torch.arange(128, dtype=torch.int32))
+
+
+def test_every_struct_field_offset_matches_the_c_compiler(tmp_path):
+    """gcc compiles the header and prints offsetof / sizeof of every field of pa_attn_args,
+    pa_mask and pa_term; the ctypes mirrors must agree field by field."""
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    structs = {"pa_attn_args": _lib.PaAttnArgs, "pa_mask": _lib.PaMask, "pa_term": _lib.PaTerm}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("  return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-o", str(exe), str(src)], check=True, capture_output=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    seen = 0
+    for line in filter(None, out):
+        cname, field, val = line.split()
+        cls = structs[cname]
+        want = ctypes.sizeof(cls) if field == "sizeof" else getattr(cls, field).offset
+        assert int(val) == want, f"{cname}.{field}: C {val}, ctypes {want}"
+        seen += 1
+    assert seen == sum(len(c._fields_) + 1 for c in structs.values())
