@@ -40,13 +40,22 @@ struct StepDesc {
 static_assert(sizeof(StepDesc) == 64, "descriptor is 16 words");
 
 typedef __attribute__((address_space(3))) char lds_char_t;
+typedef const __attribute__((address_space(3))) char* lds_cptr;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(3))) u32x4 lds_u4;
+typedef const __attribute__((address_space(3))) uint32_t lds_u32;
 
-// One LDS stage: V rows (64 x 256 B), K rows (64 x 256 B), 4 bitmap slots of 128 words.
-constexpr int kStV = 0;
-constexpr int kStK = 16384;
-constexpr int kStB = 32768;
-constexpr int kStBytes = 34816;
-constexpr int kStreamSmem = 2 * kStBytes;
+// LDS layout: two bitmap slots (4 x 128 words each), a ring of two V slots and a ring of
+// two K slots (64 rows x 256 B each).  K and V have separate rings because a step's
+// K is consumed one iteration before its V (the QK of step j + 1 runs beside the P.V
+// of step j).  Every read offset (slot, block, chunk) fits a DS instruction's 16-bit
+// immediate on top of a per-lane base register.
+constexpr int kBits = 0;
+constexpr int kBitsSlot = 2048;
+constexpr int kVring = 4096;
+constexpr int kKring = 36864;
+constexpr int kSlot = 16384;
+constexpr int kStreamSmem = kKring + 2 * kSlot;
 
 // LDS DMA of 16 bytes per lane (lane l writes LDS[m0 + 16 l]) / 4 bytes per lane.
 __device__ __forceinline__ void dma_x4(uint32_t m0, const char* gbase, uint32_t voff) {
@@ -128,23 +137,30 @@ void attn_stream_kernel(const AttnK a) {
   // column; A = 16 -> wave w moves all 128 rows of segment w's word column
   const uint32_t b_goff = A >= 32 ? (uint32_t)((64 * (w & 1) + lane) * wpr * 4) : (uint32_t)(lane * 4);
 
-  // ---- LDS read geometry (loop invariant; stage / block / row offsets are immediates)
+  // ---- LDS read geometry (loop invariant; slot / block / chunk offsets are immediates)
   // QK: lane (m, G) reads K row 32 lb + m, unit 2 kc + G.
-  // (pointers, not integer offsets: inbounds pointer arithmetic lets the stage, block
-  // and row constants fold into the instructions' offset fields)
-  const char* kptr[NQF];
+  lds_cptr lds = (lds_cptr)smem;
+  lds_cptr kptr[NQF];
 #pragma unroll
-  for (int kc = 0; kc < NQF; ++kc) kptr[kc] = smem + kStK + m * 256 + 16 * ((2 * kc + G) ^ (m & 15));
+  for (int kc = 0; kc < NQF; ++kc) {
+    kptr[kc] = lds + kKring + m * 256 + 16 * ((2 * kc + G) ^ (m & 15));
+    // (opaque to the compiler, so each address stays whole in one register instead of
+    // being rebuilt from shared parts at every read)
+    asm volatile("" : "+v"(kptr[kc]));
+  }
   // PV: transposed reads of V rows 32 lb + 16 c + 4 G + j16 / 4 (+8), columns
   // 32 db + 16 h16 + 4 (j16 % 4) .. +3; row % 4 = j16 / 4 fixes the swizzle.
   const int j16 = lane & 15;
   const int h16 = (lane >> 4) & 1;
-  const char* vptr[NDB];
+  lds_cptr vptr[NDB];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
-    vptr[db] = smem + kStV + (4 * G + (j16 >> 2)) * 256 +
+  for (int db = 0; db < NDB; ++db) {
+    vptr[db] = lds + kVring + (4 * G + (j16 >> 2)) * 256 +
                16 * ((4 * db + 2 * h16 + ((j16 & 3) >> 1)) ^ (4 * (j16 >> 2))) + 8 * (j16 & 1);
-  const char* bptr = smem + kStB + (w * 32 + m) * 4;  // this lane's word in bitmap slot 0
+    asm volatile("" : "+v"(vptr[db]));
+  }
+  lds_cptr bptr = lds + kBits + (w * 32 + m) * 4;  // this lane's word in a bitmap slot
+  asm volatile("" : "+v"(bptr));
 
   // ---- Q fragments (B operand of S^T = K Q^T) --------------------------------
   Frag qf[NQF];
@@ -186,144 +202,294 @@ void attn_stream_kernel(const AttnK a) {
     r.boff[3] = c[8];
     return r;
   };
-  StepDesc d_cur{}, d_nxt{};
-  if (n_steps > 0) d_cur = load_desc(0);
-  if (n_steps > 1) d_nxt = load_desc(1);
+  // This wave's view of a step: bit t = segment t has a live pair / is all live.
+  struct Flags {
+    uint32_t live, full;
+  };
+  auto flags_of = [&](uint32_t code) __attribute__((always_inline)) -> Flags {
+    const uint32_t cw = code >> (2 * w);
+    return Flags{(cw & 1u) | ((cw >> 7) & 2u) | ((cw >> 14) & 4u) | ((cw >> 21) & 8u),
+                 ((cw >> 1) & 1u) | ((cw >> 8) & 2u) | ((cw >> 15) & 4u) | ((cw >> 22) & 8u)};
+  };
 
-  // Issue the DMA of step descriptor `dd` into stage SB.  A past-the-list segment loads
-  // row 0 (valid memory); its code is 0, so no wave reads its K scores unmasked or
-  // multiplies its V rows (a P.V chunk of a segment dead for the wave is skipped).
-#define PA_ISSUE(dd, SB)                                                                          \
+  // DMA of a step's K rows and bitmaps (slot SL of the K ring and of the bitmap slots)
+  // and of its V rows (slot SL of the V ring).  A past-the-list segment loads row 0
+  // (valid memory); its code is 0, so no wave reads its scores unmasked or multiplies
+  // its V rows.
+#define PA_SEG_ROW(dd, t)                                                                         \
+  ((dd).base[t] < 0 ? 0                                                                           \
+   : gather_kv      ? ((dd).base[t] & rmask) * a.residue_s + ((dd).base[t] >> a.residue_qlog2)    \
+                    : (dd).base[t])
+#define PA_DMA_K(dd, SL)                                                                          \
   do {                                                                                            \
-    _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                               \
-      const int b0 = (dd).base[t];                                                                \
-      const int g = b0 < 0 ? 0 : gather_kv ? (b0 & rmask) * a.residue_s + (b0 >> a.residue_qlog2) : b0; \
-      const uint32_t rowoff = (uint32_t)((SB) * kStBytes + (16 * t + 4 * w) * 256);               \
-      dma_x4(lds0 + rowoff + kStK, kbase + (uint32_t)g * krow_b32, k_goff);                       \
-      dma_x4(lds0 + rowoff + kStV, vbase + (uint32_t)g * vrow_b32, v_goff);                       \
-    }                                                                                             \
+    _Pragma("unroll") for (int t = 0; t < 4; ++t)                                                 \
+      dma_x4(lds0 + kKring + (SL) * kSlot + (16 * t + 4 * w) * 256,                               \
+             kbase + (uint32_t)PA_SEG_ROW(dd, t) * krow_b32, k_goff);                             \
     if (A >= 32) {                                                                                \
       const int lbw = w >> 1;                                                                     \
       const int off = lbw == 0 ? (dd).boff[0] : (dd).boff[2];                                     \
       if (off >= 0)                                                                               \
-        dma_x1(lds0 + (SB) * kStBytes + kStB + lbw * 1024 + (w & 1) * 256, bits + (int64_t)off * 4, \
+        dma_x1(lds0 + kBits + (SL) * kBitsSlot + lbw * 1024 + (w & 1) * 256, bits + (int64_t)off * 4, \
                b_goff);                                                                           \
     } else {                                                                                      \
       const int off = w == 0 ? (dd).boff[0] : w == 1 ? (dd).boff[1] : w == 2 ? (dd).boff[2] : (dd).boff[3]; \
       if (off >= 0) {                                                                             \
-        dma_x1(lds0 + (SB) * kStBytes + kStB + w * 512, bits + (int64_t)off * 4, b_goff);         \
-        dma_x1(lds0 + (SB) * kStBytes + kStB + w * 512 + 256, bits + (int64_t)off * 4, b_goff + 256); \
+        dma_x1(lds0 + kBits + (SL) * kBitsSlot + w * 512, bits + (int64_t)off * 4, b_goff);       \
+        dma_x1(lds0 + kBits + (SL) * kBitsSlot + w * 512 + 256, bits + (int64_t)off * 4, b_goff + 256); \
       }                                                                                           \
     }                                                                                             \
   } while (0)
-
-  // One step on stage SB with descriptor dd: QK, mask, softmax, PV.
-#define PA_COMPUTE(dd, SB)                                                                        \
+#define PA_DMA_V(dd, SL)                                                                          \
   do {                                                                                            \
-    f32x16 s[2];                                                                                  \
-    bool blive[2], slive[4];                                                                      \
-    _Pragma("unroll") for (int lb = 0; lb < 2; ++lb) {                                            \
-      const uint32_t c0 = ((dd).code >> (16 * lb + 2 * w)) & 3u;                                  \
-      const uint32_t c1 = ((dd).code >> (16 * lb + 8 + 2 * w)) & 3u;                              \
-      const bool any0 = c0 & 1u, any1 = c1 & 1u, all0 = c0 >> 1, all1 = c1 >> 1;                  \
-      slive[2 * lb] = any0;                                                                       \
-      slive[2 * lb + 1] = any1;                                                                   \
-      blive[lb] = any0 || any1;                                                                   \
-      if (!blive[lb]) continue;                                                                   \
-      s[lb] = Mma<T>::mma(__builtin_bit_cast(Frag, *reinterpret_cast<const uint4*>(kptr[0] + (SB) * kStBytes + lb * 8192)), \
-                          qf[0], f32x16{0});                                                      \
-      _Pragma("unroll") for (int kc = 1; kc < NQF; ++kc) {                                        \
-        const uint4 kx = *reinterpret_cast<const uint4*>(kptr[kc] + (SB) * kStBytes + lb * 8192); \
-        s[lb] = Mma<T>::mma(__builtin_bit_cast(Frag, kx), qf[kc], s[lb]);                          \
-      }                                                                                           \
-      if (!(all0 && all1)) {                                                                      \
-        uint32_t word;                                                                            \
-        if (A >= 32) {                                                                            \
-          word = *reinterpret_cast<const uint32_t*>(bptr + (SB) * kStBytes + lb * 1024);                \
-        } else {                                                                                  \
-          const uint32_t lo = all0 ? 0xffffu                                                      \
-                                   : any0 ? *reinterpret_cast<const uint32_t*>(bptr + (SB) * kStBytes + (2 * lb) * 512) & 0xffffu \
-                                          : 0u;                                                   \
-          const uint32_t hi = all1 ? 0xffffu                                                      \
-                                   : any1 ? *reinterpret_cast<const uint32_t*>(bptr + (SB) * kStBytes + (2 * lb + 1) * 512) & 0xffffu \
-                                          : 0u;                                                   \
-          word = lo | (hi << 16);                                                                 \
-        }                                                                                         \
-        word >>= 4 * G;                                                                           \
-        _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                          \
-          /* (a scalar copy: bit-casting the vector element itself reads element 0) */           \
-          const float sv = s[lb][i];                                                              \
-          const int32_t keep = __builtin_amdgcn_sbfe((int32_t)word, 8 * (i >> 2) + (i & 3), 1);   \
-          s[lb][i] = __builtin_bit_cast(float, (__builtin_bit_cast(int32_t, sv) & keep) |         \
-                                                   (int32_t)(0xff800000u & ~(uint32_t)keep));     \
-        }                                                                                         \
-      }                                                                                           \
+    _Pragma("unroll") for (int t = 0; t < 4; ++t)                                                 \
+      dma_x4(lds0 + kVring + (SL) * kSlot + (16 * t + 4 * w) * 256,                               \
+             vbase + (uint32_t)PA_SEG_ROW(dd, t) * vrow_b32, v_goff);                             \
+  } while (0)
+
+  // QK of both blocks of the step in K slot SL: 4 K reads ahead, then one read per MFMA
+  // (the order is spelled out for the scheduler: left alone it trades the overlap for
+  // registers and waits on every read).
+#define PA_QK(S0, S1, SL)                                                                         \
+  do {                                                                                            \
+    u32x4 ka[NQF], kb[NQF];                                                                       \
+    _Pragma("unroll") for (int kc = 0; kc < NQF; ++kc) ka[kc] = *(lds_u4*)(kptr[kc] + (SL) * kSlot); \
+    _Pragma("unroll") for (int kc = 0; kc < NQF; ++kc) kb[kc] = *(lds_u4*)(kptr[kc] + (SL) * kSlot + 8192); \
+    S0 = Mma<T>::mma(__builtin_bit_cast(Frag, ka[0]), qf[0], f32x16{0});                           \
+    _Pragma("unroll") for (int kc = 1; kc < NQF; ++kc)                                            \
+      S0 = Mma<T>::mma(__builtin_bit_cast(Frag, ka[kc]), qf[kc], S0);                              \
+    S1 = Mma<T>::mma(__builtin_bit_cast(Frag, kb[0]), qf[0], f32x16{0});                           \
+    _Pragma("unroll") for (int kc = 1; kc < NQF; ++kc)                                            \
+      S1 = Mma<T>::mma(__builtin_bit_cast(Frag, kb[kc]), qf[kc], S1);                              \
+  } while (0)
+#define PA_QK_ORDER()                                                                             \
+  do {                                                                                            \
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);                                            \
+    _Pragma("unroll") for (int q_ = 0; q_ < 2 * NQF - 4; ++q_) {                                  \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                          \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                          \
     }                                                                                             \
-    if (blive[0] || blive[1]) {                                                                   \
-      float mx = -INFINITY;                                                                       \
-      _Pragma("unroll") for (int lb = 0; lb < 2; ++lb) if (blive[lb]) {                           \
-        _Pragma("unroll") for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s[lb][i], s[lb][i + 1])); \
-      }                                                                                           \
-      mx = row_max(mx);                                                                           \
-      const float m_new = fmaxf(m_run, mx * cexp);                                                \
-      if (__ballot(m_new > m_run + kLazy) != 0ull) {                                              \
-        const float alpha = exp2f(m_run - m_new);                                                 \
-        m_run = m_new;                                                                            \
-        l_part *= alpha;                                                                          \
-        _Pragma("unroll") for (int i = 0; i < NDB; ++i) acc[i] *= alpha;                          \
-      }                                                                                           \
-      const float neg_m = -m_run;                                                                 \
-      _Pragma("unroll") for (int lb = 0; lb < 2; ++lb) {                                          \
-        if (!blive[lb]) continue;                                                                 \
-        _Pragma("unroll") for (int c = 0; c < 2; ++c) {                                           \
-          if (!slive[2 * lb + c]) continue;                                                       \
-          f32x8 pv;                                                                               \
-          _Pragma("unroll") for (int e = 0; e < 8; ++e)                                           \
-            pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[lb][8 * c + e], cexp, neg_m));         \
-          const Frag pf = Mma<T>::cvt(pv);                                                        \
-          const uint4 pw = __builtin_bit_cast(uint4, pf);                                         \
-          l_part = dot2_sum<T>(pw.x, l_part);                                                     \
-          l_part = dot2_sum<T>(pw.y, l_part);                                                     \
-          l_part = dot2_sum<T>(pw.z, l_part);                                                     \
-          l_part = dot2_sum<T>(pw.w, l_part);                                                     \
-          _Pragma("unroll") for (int db = 0; db < NDB; ++db) {                                    \
-            const char* v1 = vptr[db] + (SB) * kStBytes + (32 * lb + 16 * c) * 256;               \
-            const s16x4 x1 = lds_read_tr(v1);                                                     \
-            const s16x4 x2 = lds_read_tr(v1 + 8 * 256);                                           \
-            const uint4 vx = {__builtin_bit_cast(uint2, x1).x, __builtin_bit_cast(uint2, x1).y,  \
-                              __builtin_bit_cast(uint2, x2).x, __builtin_bit_cast(uint2, x2).y};  \
-            acc[db] = Mma<T>::mma(__builtin_bit_cast(Frag, vx), pf, acc[db]);                      \
-          }                                                                                       \
-        }                                                                                         \
-      }                                                                                           \
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                            \
+  } while (0)
+
+  // Mask block lb of S (some pairs dead for this wave) from bitmap slot BS: bit c of the
+  // lane's row word is kv column c of the block; element i of S is column 8 (i / 4) +
+  // 4 G + i % 4.
+#define PA_MASK(S, BS, lb, fl)                                                                    \
+  do {                                                                                            \
+    uint32_t word;                                                                                \
+    if (A >= 32) {                                                                                \
+      word = *(lds_u32*)(bptr + (BS) * kBitsSlot + (lb) * 1024);                                  \
+    } else {                                                                                      \
+      const uint32_t t0 = 2 * (lb), t1 = 2 * (lb) + 1;                                            \
+      const uint32_t lo = ((fl).full >> t0) & 1u ? 0xffffu                                        \
+                          : ((fl).live >> t0) & 1u ? *(lds_u32*)(bptr + (BS) * kBitsSlot + t0 * 512) & 0xffffu \
+                                                   : 0u;                                          \
+      const uint32_t hi = ((fl).full >> t1) & 1u ? 0xffffu                                        \
+                          : ((fl).live >> t1) & 1u ? *(lds_u32*)(bptr + (BS) * kBitsSlot + t1 * 512) & 0xffffu \
+                                                   : 0u;                                          \
+      word = lo | (hi << 16);                                                                     \
+    }                                                                                             \
+    word >>= 4 * G;                                                                               \
+    _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                              \
+      /* (a scalar copy: bit-casting the vector element itself reads element 0) */               \
+      const float sv = S[i];                                                                      \
+      const int32_t keep = __builtin_amdgcn_sbfe((int32_t)word, 8 * (i >> 2) + (i & 3), 1);       \
+      S[i] = __builtin_bit_cast(float, (__builtin_bit_cast(int32_t, sv) & keep) |                 \
+                                           (int32_t)(0xff800000u & ~(uint32_t)keep));             \
     }                                                                                             \
   } while (0)
 
-  // One step jj on stage SB: wait for this step's data, start the next step's DMA into
-  // the other stage (free: every wave has passed the barrier, so finished step jj - 1),
-  // fetch the descriptor two steps ahead, compute.
-#define PA_STEP(jj, SB)                                                                           \
+  // Bring block lb of freshly computed scores to what the softmax may see: -inf for a
+  // block dead for this wave, masked for a partial one, unchanged when full.
+#define PA_SHAPE(S, BS, lb, fl)                                                                   \
+  do {                                                                                            \
+    const uint32_t bm = 3u << (2 * (lb));                                                         \
+    if (!((fl).live & bm)) {                                                                      \
+      _Pragma("unroll") for (int i = 0; i < 16; ++i) S[i] = -INFINITY;                            \
+    } else if (((fl).full & bm) != bm) {                                                          \
+      PA_MASK(S, BS, lb, fl);                                                                     \
+    }                                                                                             \
+  } while (0)
+
+  // Row maximum over the live blocks of the next step, raised into m_run lazily (after
+  // that step's predecessor has been accumulated at the old maximum).
+#define PA_BLOCK_MAX(mx, S)                                                                       \
+  _Pragma("unroll") for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(S[i], S[i + 1]))
+#define PA_RAISE(mx)                                                                              \
+  do {                                                                                            \
+    const float m_new = fmaxf(m_run, row_max(mx) * cexp);                                         \
+    if (__ballot(m_new > m_run + kLazy) != 0ull) {                                                \
+      const float alpha = exp2f(m_run - m_new);                                                   \
+      m_run = m_new;                                                                              \
+      l_part *= alpha;                                                                            \
+      _Pragma("unroll") for (int i = 0; i < NDB; ++i) acc[i] *= alpha;                            \
+    }                                                                                             \
+  } while (0)
+
+  // P of chunk c (16 kv rows) of block S: exp2(S c - m), packed, summed into l_part.
+#define PA_EXP(PF, S, c)                                                                          \
+  do {                                                                                            \
+    f32x8 pv;                                                                                     \
+    _Pragma("unroll") for (int e = 0; e < 8; ++e)                                                 \
+      pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[8 * (c) + e], cexp, neg_m));                 \
+    PF = Mma<T>::cvt(pv);                                                                         \
+    const uint4 pw = __builtin_bit_cast(uint4, PF);                                               \
+    l_part = dot2_sum<T>(pw.x, l_part);                                                           \
+    l_part = dot2_sum<T>(pw.y, l_part);                                                           \
+    l_part = dot2_sum<T>(pw.z, l_part);                                                           \
+    l_part = dot2_sum<T>(pw.w, l_part);                                                           \
+  } while (0)
+  // P.V of chunk c of block lb from V slot SL.
+#define PA_PV(PF, SL, lb, c)                                                                      \
+  do {                                                                                            \
+    _Pragma("unroll") for (int db = 0; db < NDB; ++db) {                                          \
+      lds_cptr v1 = vptr[db] + (SL) * kSlot + (32 * (lb) + 16 * (c)) * 256;                       \
+      const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(v1));                  \
+      const s16x4 x2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(v1 + 8 * 256));        \
+      const uint4 vx = {__builtin_bit_cast(uint2, x1).x, __builtin_bit_cast(uint2, x1).y,         \
+                        __builtin_bit_cast(uint2, x2).x, __builtin_bit_cast(uint2, x2).y};        \
+      acc[db] = Mma<T>::mma(__builtin_bit_cast(Frag, vx), PF, acc[db]);                            \
+    }                                                                                             \
+  } while (0)
+
+  // Order of the straight-line iteration, spelled out for the scheduler: 4 K reads
+  // ahead; 16 x (QK MFMA, LDS read, 6 VALU of the exponentials); 16 x (P.V MFMA, 2
+  // transposed V reads, 1 VALU of the next maximum).  Each MFMA then runs while the
+  // wave issues the VALU work of the other half of the pipeline, and the fragments in
+  // flight stay few enough for two waves per SIMD.
+#define PA_FAST_ORDER()                                                                           \
+  do {                                                                                            \
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);                                            \
+    _Pragma("unroll") for (int q_ = 0; q_ < 2 * NQF; ++q_) {                                      \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                                          \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);                                          \
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);                                          \
+    }                                                                                             \
+    _Pragma("unroll") for (int q_ = 0; q_ < 4 * NDB; ++q_) {                                      \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                                          \
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);                                          \
+      __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);                                          \
+    }                                                                                             \
+  } while (0)
+
+  // One iteration jj (P = jj & 1), for jj + 1 < n_steps: QK of step jj + 1 (K slot P ^ 1)
+  // beside the softmax of step jj, P.V of step jj (V slot P) beside the shaping and the
+  // maximum of step jj + 1.  At entry, after the wait and the barrier, K / bitmaps of
+  // step jj + 1 and V of step jj are in LDS; the slots the new DMA writes were last read
+  // before the barrier.  A block dead for this wave holds -inf (set when its scores
+  // were made), so its P is 0 and one straight-line body serves every step.
+#define PA_ITER(jj, P)                                                                            \
   do {                                                                                            \
     dma_wait_all();                                                                               \
     __syncthreads();                                                                              \
-    if ((jj) + 1 < n_steps) PA_ISSUE(d_nxt, (SB) ^ 1);                                            \
-    StepDesc d_aft{};                                                                             \
-    if ((jj) + 2 < n_steps) d_aft = load_desc((jj) + 2);                                          \
-    PA_COMPUTE(d_cur, SB);                                                                        \
-    d_cur = d_nxt;                                                                                \
-    d_nxt = d_aft;                                                                                \
+    if ((jj) + 2 < n_steps) PA_DMA_K(d_j2, (P));                                                  \
+    PA_DMA_V(d_j1, (P) ^ 1);                                                                      \
+    StepDesc d_j3{};                                                                              \
+    if ((jj) + 3 < n_steps) d_j3 = load_desc((jj) + 3);                                           \
+    const Flags fn = flags_of(d_j1.code);                                                         \
+    const float neg_m = -m_run;                                                                   \
+    f32x16 sn0, sn1;                                                                              \
+    if (fc.live | fn.live) {                                                                      \
+      Frag pf00, pf01, pf10, pf11;                                                                \
+      PA_EXP(pf00, sc0, 0);                                                                       \
+      PA_EXP(pf01, sc0, 1);                                                                       \
+      PA_EXP(pf10, sc1, 0);                                                                       \
+      PA_EXP(pf11, sc1, 1);                                                                       \
+      PA_QK(sn0, sn1, (P) ^ 1);                                                                   \
+      PA_PV(pf00, (P), 0, 0);                                                                     \
+      PA_PV(pf01, (P), 0, 1);                                                                     \
+      PA_PV(pf10, (P), 1, 0);                                                                     \
+      PA_PV(pf11, (P), 1, 1);                                                                     \
+      PA_FAST_ORDER();                                                                            \
+    }                                                                                             \
+    PA_SHAPE(sn0, (P) ^ 1, 0, fn);                                                                \
+    PA_SHAPE(sn1, (P) ^ 1, 1, fn);                                                                \
+    if (fn.live) {                                                                                \
+      float mx = -INFINITY;                                                                       \
+      PA_BLOCK_MAX(mx, sn0);                                                                      \
+      PA_BLOCK_MAX(mx, sn1);                                                                      \
+      PA_RAISE(mx);                                                                               \
+    }                                                                                             \
+    sc0 = sn0;                                                                                    \
+    sc1 = sn1;                                                                                    \
+    fc = fn;                                                                                      \
+    d_j1 = d_j2;                                                                                  \
+    d_j2 = d_j3;                                                                                  \
   } while (0)
 
-  if (n_steps > 0) PA_ISSUE(d_cur, 0);
-  for (int j = 0; j < n_steps; j += 2) {
-    PA_STEP(j, 0);
-    if (j + 1 >= n_steps) break;
-    PA_STEP(j + 1, 1);
+  // The last step: its V (slot P) arrives, then its softmax and P.V.
+#define PA_LAST(P)                                                                                \
+  do {                                                                                            \
+    dma_wait_all();                                                                               \
+    __syncthreads();                                                                              \
+    if (fc.live) {                                                                                \
+      const float neg_m = -m_run;                                                                 \
+      Frag pf00, pf01, pf10, pf11;                                                                \
+      PA_EXP(pf00, sc0, 0);                                                                       \
+      PA_EXP(pf01, sc0, 1);                                                                       \
+      PA_EXP(pf10, sc1, 0);                                                                       \
+      PA_EXP(pf11, sc1, 1);                                                                       \
+      PA_PV(pf00, (P), 0, 0);                                                                     \
+      PA_PV(pf01, (P), 0, 1);                                                                     \
+      PA_PV(pf10, (P), 1, 0);                                                                     \
+      PA_PV(pf11, (P), 1, 1);                                                                     \
+    }                                                                                             \
+  } while (0)
+
+  // Prologue: step 0's K, bitmaps and V; then step 1's K; QK, shaping and maximum of
+  // step 0.
+  StepDesc d_j1{}, d_j2{};
+  Flags fc{0u, 0u};
+  f32x16 sc0, sc1;
+  if (n_steps > 0) {
+    const StepDesc d0 = load_desc(0);
+    if (n_steps > 1) d_j1 = load_desc(1);
+    if (n_steps > 2) d_j2 = load_desc(2);
+    PA_DMA_K(d0, 0);
+    PA_DMA_V(d0, 0);
+    dma_wait_all();
+    __syncthreads();
+    if (n_steps > 1) PA_DMA_K(d_j1, 1);
+    fc = flags_of(d0.code);
+    PA_QK(sc0, sc1, 0);
+    PA_QK_ORDER();
+    PA_SHAPE(sc0, 0, 0, fc);
+    PA_SHAPE(sc1, 0, 1, fc);
+    float mx = -INFINITY;
+    PA_BLOCK_MAX(mx, sc0);
+    PA_BLOCK_MAX(mx, sc1);
+    m_run = fmaxf(m_run, row_max(mx) * cexp);
+    // iterations 0 .. n_steps - 2 (two per trip, so every slot offset is a constant)
+    int j = 0;
+    for (; j + 1 < n_steps; j += 2) {
+      PA_ITER(j, 0);
+      if (j + 2 >= n_steps) {
+        j += 1;
+        break;
+      }
+      PA_ITER(j + 1, 1);
+    }
+    // j = n_steps - 1 now (the loop leaves with j + 1 == n_steps)
+    if (j & 1)
+      PA_LAST(1);
+    else
+      PA_LAST(0);
   }
 
-#undef PA_STEP
-#undef PA_COMPUTE
-#undef PA_ISSUE
+#undef PA_ITER
+#undef PA_LAST
+#undef PA_FAST_ORDER
+#undef PA_PV
+#undef PA_EXP
+#undef PA_RAISE
+#undef PA_BLOCK_MAX
+#undef PA_MASK
+#undef PA_SHAPE
+#undef PA_QK_ORDER
+#undef PA_QK
+#undef PA_DMA_V
+#undef PA_DMA_K
+#undef PA_SEG_ROW
 
   // ---- epilogue (as attn_fwd_kernel) -------------------------------------------
   const float l_tot = row_sum(l_part);
