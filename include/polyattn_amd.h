@@ -112,17 +112,23 @@ int pa_index_bits(const pa_mask* mask, int64_t N, int32_t BQ, int32_t A, const i
  * 64 kv columns = 4 segments of 16 columns (segment s of the list is column 16 (s mod
  * A/16) of listed tile s div (A/16)).  For query block i and step j, 16 int32 words at
  * steps[(i * steps_pitch + j) * 16]:
- *   [0..3]  index-space kv column of segment t's first column, -1 past the list
+ *   [0..3]  K / V row of segment t's first column: the index-space column b, or with
+ *           residue_s > 0 its original row (b mod 2^residue_qlog2) * residue_s +
+ *           b div 2^residue_qlog2; 0 past the list (that segment's code is 0)
  *   [4]     byte t = codes of segment t for the 4 row groups of 32 query rows:
  *           bit 2g = some pair live, bit 2g+1 = every pair live (from kv_wave_bits, or
  *           from kv_partial when that is NULL: 0x55 partial, 0xff full)
  *   [5..8]  pool word offset of the bitmap word holding segment t's columns
  *           (kv_bits_off + (16 (s mod A/16)) / 32), -1 when the tile has no bitmap
- *   [9..15] zero
- * steps_pitch >= ceil(pitch * A / 64).  kv_wave_bits and kv_bits_off may be NULL. */
+ *   [9..14] zero
+ *   [15]    residue_s (0 for rows in index space)
+ * steps_pitch >= ceil(pitch * A / 64).  kv_wave_bits and kv_bits_off may be NULL.
+ * A launch that gathers K / V through the residue basis (gather_kv, residue_s) needs
+ * steps built with the same residue_s; any other launch needs residue_s = 0. */
 int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
                    const uint32_t* kv_wave_bits, const int32_t* kv_bits_off, int64_t pitch, int64_t N,
-                   int32_t BQ, int32_t A, int32_t* steps, int64_t steps_pitch, void* stream);
+                   int32_t BQ, int32_t A, int32_t residue_s, int32_t residue_qlog2, int32_t* steps,
+                   int64_t steps_pitch, void* stream);
 
 /* ---- class-A permutation (replaces gpu/permute.py:12-31) -------------------------
  * Row gather dst[b, p, :] = src[b, perm[p], :] (inverse = 0), the index_select of

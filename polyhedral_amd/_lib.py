@@ -51,7 +51,8 @@ SIGNATURES = {
     "pa_index_compact": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp]),
     "pa_index_bits": (ctypes.c_int, [ctypes.POINTER(PaMask), c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i64, c_vp,
                                      c_vp, c_vp, c_vp]),
-    "pa_index_steps": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
+    "pa_index_steps": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp,
+                                      c_i64, c_vp]),
     "pa_permute_rows": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                        c_i32, c_vp]),
     "pa_invert_perm": (ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),

@@ -118,6 +118,11 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
     PA_CHECK_ARG(x->steps_pitch >= (x->pitch * x->A + 63) / 64, "pa_attn_fwd: steps_pitch=%lld < %lld",
                  (long long)x->steps_pitch, (long long)((x->pitch * x->A + 63) / 64));
     PA_CHECK_ARG((reinterpret_cast<uintptr_t>(x->kv_steps) & 15) == 0, "pa_attn_fwd: kv_steps not 16-byte aligned");
+    {
+      // row offsets inside a head are 32-bit in the streaming kernel
+      const int64_t rb = (x->k_sn > x->v_sn ? x->k_sn : x->v_sn) * 2;
+      PA_CHECK_ARG(x->N * rb < (1ll << 31), "pa_attn_fwd: N * row stride too large for kv_steps");
+    }
     return pa::launch_attn_stream(a, x->dtype, s);
   }
   switch (x->dtype) {

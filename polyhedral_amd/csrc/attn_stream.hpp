@@ -32,7 +32,7 @@
 namespace pa {
 
 struct StepDesc {
-  int32_t base[4];  // index-space kv column of each 16-column segment, -1 past the list
+  int32_t base[4];  // K / V row of each 16-column segment (gather basis applied), 0 past the list
   uint32_t code;    // byte t: segment t's 2-bit codes for the 4 row groups
   int32_t boff[4];  // pool word offset of the bitmap word of segment t, -1 when none
   int32_t pad[7];
@@ -213,13 +213,10 @@ void attn_stream_kernel(const AttnK a) {
   };
 
   // DMA of a step's K rows and bitmaps (slot SL of the K ring and of the bitmap slots)
-  // and of its V rows (slot SL of the V ring).  A past-the-list segment loads row 0
-  // (valid memory); its code is 0, so no wave reads its scores unmasked or multiplies
-  // its V rows.
-#define PA_SEG_ROW(dd, t)                                                                         \
-  ((dd).base[t] < 0 ? 0                                                                           \
-   : gather_kv      ? ((dd).base[t] & rmask) * a.residue_s + ((dd).base[t] >> a.residue_qlog2)    \
-                    : (dd).base[t])
+  // and of its V rows (slot SL of the V ring).  The descriptor holds each segment's K / V
+  // row already mapped through the gather basis; a past-the-list segment loads row 0
+  // (valid memory) and has code 0, so its scores are -inf and its P is 0.
+#define PA_SEG_ROW(dd, t) ((dd).base[t])
 #define PA_DMA_K(dd, SL)                                                                          \
   do {                                                                                            \
     _Pragma("unroll") for (int t = 0; t < 4; ++t)                                                 \
@@ -353,8 +350,9 @@ void attn_stream_kernel(const AttnK a) {
   } while (0)
 
   // Order of the straight-line iteration, spelled out for the scheduler: 4 K reads
-  // ahead; 16 x (QK MFMA, LDS read, 6 VALU of the exponentials); 16 x (P.V MFMA, 2
-  // transposed V reads, 1 VALU of the next maximum).  Each MFMA then runs while the
+  // ahead; 16 x (QK MFMA, LDS read, 6 VALU of the exponentials); 4 more reads, so the
+  // transposed V reads run 4 MFMAs ahead; 12 x (P.V MFMA, 2 reads, 1 VALU); 4 x (P.V
+  // MFMA, 1 VALU).  Each MFMA then runs while the
   // wave issues the VALU work of the other half of the pipeline, and the fragments in
   // flight stay few enough for two waves per SIMD.
 #define PA_FAST_ORDER()                                                                           \
@@ -365,9 +363,14 @@ void attn_stream_kernel(const AttnK a) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);                                          \
       __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);                                          \
     }                                                                                             \
-    _Pragma("unroll") for (int q_ = 0; q_ < 4 * NDB; ++q_) {                                      \
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);                                            \
+    _Pragma("unroll") for (int q_ = 0; q_ < 4 * NDB - 4; ++q_) {                                  \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                                          \
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);                                          \
+      __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);                                          \
+    }                                                                                             \
+    _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                            \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                                          \
       __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);                                          \
     }                                                                                             \
   } while (0)

@@ -293,8 +293,9 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(const int32_t* __restri
                                                           const int8_t* __restrict__ kv_partial,
                                                           const uint32_t* __restrict__ kv_wave_bits,
                                                           const int32_t* __restrict__ kv_bits_off, int64_t pitch,
-                                                          int32_t nq, int32_t BQ, int32_t A,
-                                                          int32_t* __restrict__ steps, int64_t steps_pitch) {
+                                                          int32_t nq, int32_t BQ, int32_t A, int32_t residue_s,
+                                                          int32_t residue_qlog2, int32_t* __restrict__ steps,
+                                                          int64_t steps_pitch) {
   const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (gid >= (int64_t)nq * steps_pitch) return;
   const int qb = (int)(gid / steps_pitch);
@@ -310,12 +311,16 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(const int32_t* __restri
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int seg = 4 * j + t;
-    int32_t base = -1, boff = -1;
+    int32_t base = 0, boff = -1;
     uint32_t c8 = 0u;
     if (seg < n_seg) {
       const int64_t ti = (int64_t)qb * pitch + seg / spt;
       const int within = seg % spt;
       base = kv_idx[ti] * A + within * 16;
+      if (residue_s > 0) {
+        const int32_t rmask = (1 << residue_qlog2) - 1;
+        base = (base & rmask) * residue_s + (base >> residue_qlog2);
+      }
       if (kv_wave_bits) {
         const int cg = A >= 32 ? within >> 1 : 0;
         const uint32_t wb = kv_wave_bits[ti];
@@ -330,6 +335,7 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(const int32_t* __restri
     code |= c8 << (8 * t);
   }
   d[4] = (int32_t)code;
+  d[15] = residue_s > 0 ? residue_s : 0;
   int4* dst = reinterpret_cast<int4*>(steps + gid * 16);
 #pragma unroll
   for (int i = 0; i < 4; ++i) dst[i] = int4{d[4 * i], d[4 * i + 1], d[4 * i + 2], d[4 * i + 3]};
@@ -340,12 +346,17 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(const int32_t* __restri
 
 extern "C" int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
                               const uint32_t* kv_wave_bits, const int32_t* kv_bits_off, int64_t pitch, int64_t N,
-                              int32_t BQ, int32_t A, int32_t* steps, int64_t steps_pitch, void* stream) {
+                              int32_t BQ, int32_t A, int32_t residue_s, int32_t residue_qlog2, int32_t* steps,
+                              int64_t steps_pitch, void* stream) {
   PA_CHECK_ARG(kv_num, "pa_index_steps: null kv_num");
   PA_CHECK_ARG(N >= 1 && N <= (1ll << 30), "pa_index_steps: N=%lld out of range", (long long)N);
   PA_CHECK_ARG(pa::tile_ok(BQ) && pa::tile_ok(A) && N % BQ == 0 && N % A == 0,
                "pa_index_steps: bad tile shape BQ=%d A=%d for N=%lld", BQ, A, (long long)N);
   PA_CHECK_ARG(pitch >= 0, "pa_index_steps: negative pitch");
+  PA_CHECK_ARG(residue_s <= 0 || (residue_qlog2 >= 4 && residue_qlog2 < 31 &&
+                                  (int64_t)residue_s << residue_qlog2 == N),
+               "pa_index_steps: residue_s=%d with N/s = 2^%d does not match N=%lld", residue_s, residue_qlog2,
+               (long long)N);
   PA_CHECK_ARG(steps_pitch >= (pitch * A + 63) / 64,
                "pa_index_steps: steps_pitch=%lld < ceil(pitch * A / 64) = %lld", (long long)steps_pitch,
                (long long)((pitch * A + 63) / 64));
@@ -358,7 +369,8 @@ extern "C" int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, cons
   PA_CHECK_ARG(total / pa::kThreads < 0x7fffffffll, "pa_index_steps: too many steps");
   hipLaunchKernelGGL(pa::steps_kernel, dim3((unsigned)((total + pa::kThreads - 1) / pa::kThreads)),
                      dim3(pa::kThreads), 0, static_cast<hipStream_t>(stream), kv_idx, kv_num, kv_partial,
-                     kv_wave_bits, kv_bits_off, pitch, (int32_t)nq, BQ, A, steps, steps_pitch);
+                     kv_wave_bits, kv_bits_off, pitch, (int32_t)nq, BQ, A, residue_s > 0 ? residue_s : 0,
+                     residue_qlog2, steps, steps_pitch);
   PA_LAUNCH_CHECK("steps_kernel");
   return PA_OK;
 }

@@ -42,9 +42,12 @@ def _register(kv_idx, BQ, A, **arrays):
     key = id(kv_idx)
     entry = _EXTRAS.get(key)
     if entry is None or entry[0]() is not kv_idx:
-        entry = (weakref.ref(kv_idx), dict(BQ=BQ, A=A))
+        entry = (weakref.ref(kv_idx), dict(BQ=BQ, A=A, steps={}))
         _EXTRAS[key] = entry
         weakref.finalize(kv_idx, _EXTRAS.pop, key, None)
+    steps = arrays.pop("steps", None)
+    if steps:
+        entry[1]["steps"].update(steps)
     entry[1].update(arrays)
 
 
@@ -55,18 +58,27 @@ def _extras(kv_idx, BQ, A):
     return entry[1]
 
 
-def build_steps(kv_idx, kv_num, kv_partial, wave, bits_off, N, BQ, A):
-    """Step descriptors [N/BQ, ceil(pitch * A / 64), 16] int32 (pa_index_steps), or None
-    for an index whose every list is empty."""
+def build_steps(kv_idx, kv_num, kv_partial, wave, bits_off, N, BQ, A, residue=0):
+    """Step descriptors [N/BQ, ceil(pitch * A / 64), 16] int32 (pa_index_steps) whose
+    K / V rows are in the residue-s basis (residue > 0, N / s a power of two) or in index
+    space (residue = 0); None for an index whose every list is empty.  The tensor carries
+    the basis as attribute ``residue_s``."""
     nq, pitch = kv_idx.shape
     sp = (pitch * A + 63) // 64
     if sp == 0:
         return None
+    qlog2 = 0
+    if residue:
+        qn = N // residue
+        if N % residue or qn & (qn - 1):
+            raise ValueError(f"closed-form residue basis needs N/s a power of two (N={N}, s={residue})")
+        qlog2 = qn.bit_length() - 1
     steps = torch.empty((nq, sp, 16), dtype=torch.int32, device=kv_idx.device)
     with torch.cuda.device(kv_idx.device):
         _lib.check(_lib.lib().pa_index_steps(_lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial),
-                                             _lib.ptr(wave), _lib.ptr(bits_off), pitch, N, BQ, A,
-                                             _lib.ptr(steps), sp, _lib.stream_of(steps)), "pa_index_steps")
+                                             _lib.ptr(wave), _lib.ptr(bits_off), pitch, N, BQ, A, int(residue),
+                                             qlog2, _lib.ptr(steps), sp, _lib.stream_of(steps)), "pa_index_steps")
+    steps.residue_s = int(residue)
     return steps
 
 
@@ -104,14 +116,15 @@ def _default_device(device):
     return torch.device(device)
 
 
-def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None, bits=False, steps=False):
+def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None, bits=False, steps=False,
+                 residue=0):
     """Build on the GPU; returns (kv_idx, kv_num, kv_partial, kv_wave_bits, tiles, live) with
     device tensors and host ints.  One synchronisation (to size the padded lists).
 
     bits=True appends (kv_bits_off, kv_bits): element bitmaps of the partial tiles
     (pa_index_bits), so the attention kernel masks by table lookup.  steps=True (which
     implies bits) appends the step descriptors of the streaming kernel (None when every
-    list is empty)."""
+    list is empty), with K / V rows in the residue-``residue`` basis (0: index space)."""
     bits = bits or steps
     assert N % BQ == 0 and N % A == 0
     dev = _default_device(device)
@@ -147,9 +160,9 @@ def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None, bits=F
             out = out + ((off, pool),)
             _register(kv_idx, BQ, A, bits=(off, pool))
         if steps:
-            st = build_steps(kv_idx, kv_num, kv_partial, wave, out[6][0], N, BQ, A)
+            st = build_steps(kv_idx, kv_num, kv_partial, wave, out[6][0], N, BQ, A, residue)
             out = out + (st,)
-            _register(kv_idx, BQ, A, steps=st)
+            _register(kv_idx, BQ, A, steps={int(residue): st}, N=N, arrays=(kv_num, kv_partial, wave))
     _register(kv_idx, BQ, A, wave=wave)
     return out
 
@@ -186,7 +199,17 @@ def wave_bits_for(kv_idx, BQ, A):
     return wave if wave is not None and wave.shape == kv_idx.shape else None
 
 
-def stream_arrays_for(kv_idx, BQ, A):
-    """(bitmaps, step descriptors) registered for this kv_idx tensor, or (None, None)."""
+def stream_arrays_for(kv_idx, BQ, A, residue=0):
+    """(bitmaps, step descriptors in the residue basis) registered for this kv_idx tensor,
+    building the descriptors for a new basis from the registered index arrays; (None,
+    None) when the index was not built with bitmaps."""
     ex = _extras(kv_idx, BQ, A)
-    return ex.get("bits"), ex.get("steps")
+    bits = ex.get("bits")
+    if bits is None:
+        return None, None
+    steps = ex["steps"].get(int(residue))
+    if steps is None and "arrays" in ex:
+        kv_num, kv_partial, wave = ex["arrays"]
+        steps = build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], ex["N"], BQ, A, residue)
+        ex["steps"][int(residue)] = steps
+    return bits, steps

@@ -65,7 +65,8 @@ class SplitPlan:
                           else torch.from_numpy(np.asarray(p.perm, dtype=np.int32)).to(dev))
             mask = Permuted(p.mask, perm_t.cpu().numpy()) if perm_t is not None else p.mask
             stream = (p.BQ, p.A) in STREAM_TILES
-            built = build_device(mask, N, p.BQ, p.A, device=dev, bits=True, steps=stream)
+            built = build_device(mask, N, p.BQ, p.A, device=dev, bits=True, steps=stream,
+                                 residue=_closed_form_residue(p, N))
             kv_idx, kv_num, kv_partial, wave, tiles, live, bits = built[:7]
             steps = built[7] if stream else None
             inc, exc = p.mask.terms()

@@ -20,7 +20,7 @@ STREAM_MASKS = ["window-128", "causal", "dilated-8", "local256+str8", "twoband-1
                 "prefixlm-2048", "lat16-band256"]
 
 
-def _expected_steps(kv_idx, kv_num, wave, bits_off, BQ, A):
+def _expected_steps(kv_idx, kv_num, wave, bits_off, BQ, A, N=0, residue=0):
     """The descriptor layout of include/polyattn_amd.h (pa_index_steps), from the index."""
     nq, pitch = kv_idx.shape
     spt = A // 16
@@ -34,10 +34,13 @@ def _expected_steps(kv_idx, kv_num, wave, bits_off, BQ, A):
             code = 0
             for t in range(4):
                 seg = 4 * j + t
-                base, boff, c8 = -1, -1, 0
+                base, boff, c8 = 0, -1, 0
                 if seg < n_seg:
                     ti, within = seg // spt, seg % spt
                     base = int(kv_idx[qb, ti]) * A + within * 16
+                    if residue:
+                        q = N // residue
+                        base = (base % q) * residue + base // q
                     cg = within >> 1 if A >= 32 else 0
                     wb = int(wave[qb, ti]) & 0xFFFFFFFF
                     for g in range(min(ngr, 4)):
@@ -48,17 +51,20 @@ def _expected_steps(kv_idx, kv_num, wave, bits_off, BQ, A):
                 out[qb, j, 5 + t] = boff
                 code |= c8 << (8 * t)
             out[qb, j, 4] = code
+            out[qb, j, 15] = residue
     return (out & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
 
 
+@pytest.mark.parametrize("residue", [0, 16])
 @pytest.mark.parametrize("A", [16, 32, 64])
 @pytest.mark.parametrize("name", ["window-128", "dilated-8", "lat16-band256", "sinks4+win8"])
-def test_step_descriptors_follow_the_index(gpu, name, A):
+def test_step_descriptors_follow_the_index(gpu, name, A, residue):
     N, BQ = 2048, 128
     kv_idx, kv_num, kv_partial, wave, tiles, live, bits, steps = pindex.build_device(
-        numpy_mask(name), N, BQ, A, device=gpu, bits=True, steps=True)
+        numpy_mask(name), N, BQ, A, device=gpu, bits=True, steps=True, residue=residue)
+    assert steps.residue_s == residue
     want = _expected_steps(kv_idx.cpu().numpy(), kv_num.cpu().numpy(), wave.cpu().numpy(),
-                           bits[0].cpu().numpy(), BQ, A)
+                           bits[0].cpu().numpy(), BQ, A, N, residue)
     got = steps.cpu().numpy()
     assert got.shape == want.shape
     assert np.array_equal(got, want), f"{name} A={A}: first mismatch at {np.argwhere(got != want)[:3]}"
