@@ -171,12 +171,6 @@ void attn_stream_kernel(const AttnK a) {
       qf[kc] = __builtin_bit_cast(Frag, *reinterpret_cast<const uint4*>(qrow + (16 * kc + 8 * G) * ESZ));
   }
 
-  // The compiler counts its own vector loads in vmcnt and would place the waits for Q
-  // at the first use, inside the loop, where they would also wait for the DMA of the
-  // next step; using the fragments here makes it wait once, before the loop.
-#pragma unroll
-  for (int kc = 0; kc < NQF; ++kc) asm volatile("" ::"v"(qf[kc]));
-
   f32x16 acc[NDB];
 #pragma unroll
   for (int i = 0; i < NDB; ++i) acc[i] = f32x16{0};
@@ -420,11 +414,14 @@ void attn_stream_kernel(const AttnK a) {
     d_j2 = d_j3;                                                                                  \
   } while (0)
 
-  // The last step: its V (slot P) arrives, then its softmax and P.V.
+  // The last step: its V (slot P) arrives, then its softmax and P.V.  The previous
+  // partial result the epilogue merges (2-byte types) is loaded here, after the last
+  // wait for a DMA, so its latency hides behind this step.
 #define PA_LAST(P)                                                                                \
   do {                                                                                            \
     dma_wait_all();                                                                               \
     __syncthreads();                                                                              \
+    PA_PREV_LOAD();                                                                               \
     if (fc.live) {                                                                                \
       const float neg_m = -m_run;                                                                 \
       Frag pf00, pf01, pf10, pf11;                                                                \
@@ -436,6 +433,22 @@ void attn_stream_kernel(const AttnK a) {
       PA_PV(pf01, (P), 0, 1);                                                                     \
       PA_PV(pf10, (P), 1, 0);                                                                     \
       PA_PV(pf11, (P), 1, 1);                                                                     \
+    }                                                                                             \
+  } while (0)
+
+  // Rows of the previous partial (prev_o, 2-byte types): 4 elements per (db, i4), the
+  // columns this lane writes in the epilogue.
+  const int srow = (a.scatter_o && has_pq) ? q_orig : r_idx;
+  const bool prev16 = a.prev_o && a.prev_dtype != PA_F32;
+  uint2 prevw[NDB * 4];
+  float prev_lse = -INFINITY;
+#define PA_PREV_LOAD()                                                                            \
+  do {                                                                                            \
+    if (a.prev_o) prev_lse = a.prev_lse[bh * a.lse_sb + srow];                                    \
+    if (prev16) {                                                                                 \
+      const char* prow_ = a.prev_o + (bh * a.prev_sb + (int64_t)srow * a.prev_sn) * 2;             \
+      _Pragma("unroll") for (int q_ = 0; q_ < NDB * 4; ++q_)                                      \
+        prevw[q_] = *reinterpret_cast<const uint2*>(prow_ + (32 * (q_ >> 2) + 8 * (q_ & 3) + 4 * G) * 2); \
     }                                                                                             \
   } while (0)
 
@@ -451,6 +464,12 @@ void attn_stream_kernel(const AttnK a) {
     PA_DMA_K(d0, 0);
     PA_DMA_V(d0, 0);
     dma_wait_all();
+    // The compiler counts its own vector loads in vmcnt and would place the waits for Q
+    // at the first use, inside the loop, where they would also wait for the DMA of the
+    // next step; using the fragments here makes it wait once, here, where the Q loads
+    // and step 0's DMA have been in flight together.
+#pragma unroll
+    for (int kc = 0; kc < NQF; ++kc) asm volatile("" ::"v"(qf[kc]));
     __syncthreads();
     if (n_steps > 1) PA_DMA_K(d_j1, 1);
     fc = flags_of(d0.code);
@@ -477,10 +496,13 @@ void attn_stream_kernel(const AttnK a) {
       PA_LAST(1);
     else
       PA_LAST(0);
+  } else {
+    PA_PREV_LOAD();
   }
 
 #undef PA_ITER
 #undef PA_LAST
+#undef PA_PREV_LOAD
 #undef PA_FAST_ORDER
 #undef PA_PV
 #undef PA_EXP
@@ -500,9 +522,8 @@ void attn_stream_kernel(const AttnK a) {
   float lse_v = has ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
   float a_own = has ? 1.f / l_tot : 0.f;
   float a_prev = 0.f;
-  const int srow = (a.scatter_o && has_pq) ? q_orig : r_idx;
   if (a.prev_o) {
-    const float lp = a.prev_lse[bh * a.lse_sb + srow];
+    const float lp = prev_lse;
     const float M = fmaxf(lse_v, lp);
     if (M == -INFINITY) {
       a_own = 0.f;
@@ -527,7 +548,17 @@ void attn_stream_kernel(const AttnK a) {
       const int d0 = 32 * db + 8 * i4 + 4 * G;
       f32x4 x = {acc[db][4 * i4], acc[db][4 * i4 + 1], acc[db][4 * i4 + 2], acc[db][4 * i4 + 3]};
       x *= a_own;
-      if (prow && a_prev != 0.f) x += a_prev * load4_any(prow + d0 * psz, a.prev_dtype);
+      if (prow && a_prev != 0.f) {
+        if (prev16) {
+          const uint2 pw = prevw[4 * db + i4];
+          const f32x4 pvv = a.prev_dtype == PA_BF16
+                                ? __builtin_convertvector(__builtin_bit_cast(bf16x4, pw), f32x4)
+                                : __builtin_convertvector(__builtin_bit_cast(f16x4, pw), f32x4);
+          x += a_prev * pvv;
+        } else {
+          x += a_prev * load4_any(prow + d0 * psz, a.prev_dtype);
+        }
+      }
       Mma<T>::store4(orow + d0 * ESZ, x);
     }
   }
