@@ -123,6 +123,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     q, k, v = wl.inputs(0, dev)
     launches, o, lse = plan.prepare(q, k, v)
     wall_ms, per_launch = measure(launches, steps, warmup)
+    kernels = ["attn_stream_kernel" if x.kernel == "stream" else "attn_fwd_kernel" for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
     for i, bi in enumerate(plan.launched):
         per[bi] = per_launch[i]
@@ -139,6 +140,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
         waste=round(plan.elements / live, 4) if live else None,
         pieces=[dict(mask=b["piece"].mask.name, BQ=b["piece"].BQ, A=b["piece"].A,
                      basis="identity" if b["perm"] is None else "permuted", tiles=b["tiles"], live=b["live"],
+                     kernel=kernels[plan.launched.index(i)] if i in plan.launched else None,
                      launch_ms=round(per[i], 5),
                      live_tflops=round(4 * wl.D * b["live"] * wl.H / (per[i] * 1e-3) / 1e12, 2) if per[i] else None)
                 for i, b in enumerate(plan.built)],
@@ -221,7 +223,8 @@ def main():
                     pieces=r["pieces"], index_build_ms=r["index_build_ms"]),
         roofline=dict(bound="mfma", achieved=r["kernel_live_tflops"], peak=r["peak_tflops"], unit="TFLOP/s",
                       frac=r["frac_peak"], traffic=_measured_traffic(r["workload"]),
-                      kernel="attn_fwd_kernel (all launches of one step)",
+                      kernel=" + ".join(sorted({p["kernel"] for p in r["pieces"] if p["kernel"]})) +
+                             " (all launches of one step)",
                       algorithmic="live FLOP = 4 * D * live pairs * heads per launch"),
         cpu_baseline=r.get("cpu_baseline"),
     )
