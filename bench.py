@@ -163,8 +163,10 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # (the untimed warmup also lets the GPU's clocks settle: over the first ~100 ms of load
+    # they are still rising, and a short warmup times that ramp)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default=None)
     ap.add_argument("--variant", default=None)
     ap.add_argument("--no-cpu", action="store_true")

@@ -183,6 +183,10 @@ typedef struct pa_attn_args {
   const int32_t* kv_steps;     /* NULL or pa_index_steps output for this index: enables the     */
   int64_t steps_pitch;         /*   streaming kernel (f16/bf16, D = 128, BQ = 128, A in 16, 32, */
                                /*   64, bitmaps for the partial tiles, no table gather of K/V)  */
+  int32_t heads_desc;          /* nonzero: heads are issued from the last to the first.  A pass */
+                               /*   that follows another over the same tensors then starts on   */
+                               /*   the heads the previous one touched last (still in cache).   */
+                               /*   Results do not depend on it.                                */
 } pa_attn_args;
 
 int pa_attn_fwd(const pa_attn_args* args, void* stream);

@@ -97,8 +97,12 @@ def block_sparse_attention(q, k, v, kv_idx, kv_num, kv_partial,
 def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=None,
             perm_q=None, perm_kv=None, gather_kv=False, gather_mult=1, gather_scatter=True,
             num_warps=4, num_stages=2, *, kv_wave_bits=None, kv_bits=None, gather_q=False, scatter_o=False,
-            residue=0, lse=None, prev=None, out=None, qblock_order=None, kv_steps=None, kernel="auto"):
-    """Validate the arguments of block_sparse_attention once and return a Launch."""
+            residue=0, lse=None, prev=None, out=None, qblock_order=None, kv_steps=None, kernel="auto",
+            heads_desc=False):
+    """Validate the arguments of block_sparse_attention once and return a Launch.
+
+    heads_desc: issue the heads from the last to the first (the results are the same; a
+    pass that follows another over the same tensors then starts where the cache is warm)."""
     BH, N, D = q.shape
     if perm_kv is None:
         perm_kv = perm_q
@@ -226,6 +230,7 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
                 or kv_steps.shape[2] != 16 or not kv_steps.is_contiguous():
             raise ValueError("kv_steps must be contiguous int32 [N/BQ, steps, 16]")
         args.kv_steps, args.steps_pitch = _lib.ptr(kv_steps), kv_steps.shape[1]
+    args.heads_desc = 1 if heads_desc else 0
     keep = [q, k, v, o, kv_idx, kv_num, kv_partial, kv_wave_bits, kv_bits, dmask, lse, prev, qblock_order,
             kv_steps]
     return Launch(args, keep, o, dev, "stream" if use_stream else "general")

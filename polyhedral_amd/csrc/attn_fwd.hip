@@ -100,6 +100,8 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   a.qblock_order = x->qblock_order;
   a.steps = x->kv_steps;
   a.steps_pitch = x->steps_pitch;
+  a.BH = x->BH;
+  a.heads_desc = x->heads_desc != 0;
   PA_CHECK_ARG(a.total_wg <= 0x7fffffffll, "pa_attn_fwd: %lld work-groups exceed the grid limit",
                (long long)a.total_wg);
 

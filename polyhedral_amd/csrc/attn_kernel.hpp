@@ -76,6 +76,8 @@ struct AttnK {
   const int32_t* qblock_order;
   const int32_t* steps;  // step descriptors (streaming kernel only)
   int64_t steps_pitch;
+  int64_t BH;
+  int32_t heads_desc;  // heads issued last to first
 };
 
 constexpr int kStep = 64;          // KV rows per staged step
@@ -206,7 +208,7 @@ void attn_fwd_kernel(const AttnK a) {
   const int m = lane & 31;  // query row within the wave
 
   const int64_t lid = xcd_remap(blockIdx.x, a.total_wg);
-  const int64_t bh = lid / a.nq;
+  const int64_t bh = a.heads_desc ? a.BH - 1 - lid / a.nq : lid / a.nq;
   const int qb_lin = (int)(lid % a.nq);
   const int qb = a.qblock_order ? a.qblock_order[qb_lin] : qb_lin;
 

@@ -100,7 +100,7 @@ void attn_stream_kernel(const AttnK a) {
   const int m = lane & 31;
 
   const int64_t lid = xcd_remap(blockIdx.x, a.total_wg);
-  const int64_t bh = lid / a.nq;
+  const int64_t bh = a.heads_desc ? a.BH - 1 - lid / a.nq : lid / a.nq;
   const int qb_lin = (int)(lid % a.nq);
   const int qb = a.qblock_order ? a.qblock_order[qb_lin] : qb_lin;
   const int A = a.A;

@@ -10,7 +10,10 @@ through pa_attn_fwd:
   (scatter_o), so no permuted copy of Q, K, V or O is ever materialised;
 * the first pass writes O and the per-row LSE; every later pass merges its own
   result with the previous one in its epilogue, in place (each output row is read
-  and written by the same lanes), so there is no separate merge pass.
+  and written by the same lanes), so there is no separate merge pass;
+* consecutive passes issue the heads in opposite orders, so that each pass starts
+  on the heads whose Q, K, V and O the previous pass touched last and the memory-side
+  cache still holds.
 
 Pieces must be disjoint (the peeling of compose.py:49-76 makes them so); the merge
 of disjoint pieces equals single-pass attention over their union.
@@ -110,7 +113,7 @@ class SplitPlan:
                 kv_wave_bits=b["wave"], kv_bits=b["bits"], gather_q=permuted, scatter_o=permuted,
                 residue=_closed_form_residue(p, N),
                 lse=lse_buf, prev=None if first else (o, lse_buf), out=o, qblock_order=b["order"],
-                kv_steps=b["steps"], kernel=self.kernel))
+                kv_steps=b["steps"], kernel=self.kernel, heads_desc=len(launches) % 2 == 1))
             self.launched.append(bi_)
             first = False
         return launches, o, lse_buf

@@ -166,3 +166,18 @@ def test_stream_dead_rows_and_empty_lists(gpu):
         assert torch.isfinite(out).all() and torch.count_nonzero(out[0, 5]) == 0
         assert torch.count_nonzero(out[0, 256:384]) == 0
         check_close(out, want, torch.bfloat16, f"stream dead rows 128x{A}")
+
+
+@pytest.mark.parametrize("kernel", ["stream", "general"])
+def test_heads_desc_gives_identical_results(gpu, kernel):
+    """Issuing the heads last-to-first changes only the order of the work-groups."""
+    N, D, name = 1024, 128, "lat16-band256"
+    q, k, v = (x.to(gpu) for x in make_qkv(3, N, D, torch.bfloat16, seed=5))
+    bi = pindex.build(numpy_mask(name), N, 128, 32)
+    outs = []
+    for desc in (False, True):
+        lse = torch.empty(3, N, device=gpu)
+        launch, out = _launch(q, k, v, bi, name, 128, 32, kernel, lse=lse, heads_desc=desc)
+        assert launch.kernel == kernel
+        outs.append((out.clone(), lse.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
