@@ -124,6 +124,8 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
       // row offsets inside a head are 32-bit in the streaming kernel
       const int64_t rb = (x->k_sn > x->v_sn ? x->k_sn : x->v_sn) * 2;
       PA_CHECK_ARG(x->N * rb < (1ll << 31), "pa_attn_fwd: N * row stride too large for kv_steps");
+      PA_CHECK_ARG(!x->prev_o || x->prev_dtype == PA_F32 || x->N * x->prev_sn * 2 < (1ll << 31),
+                   "pa_attn_fwd: N * prev row stride too large for kv_steps");
     }
     return pa::launch_attn_stream(a, x->dtype, s);
   }

@@ -42,6 +42,7 @@ static_assert(sizeof(StepDesc) == 64, "descriptor is 16 words");
 typedef __attribute__((address_space(3))) char lds_char_t;
 typedef const __attribute__((address_space(3))) char* lds_cptr;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(3))) u32x4 lds_u4;
 typedef const __attribute__((address_space(3))) uint32_t lds_u32;
 
@@ -136,6 +137,15 @@ void attn_stream_kernel(const AttnK a) {
   // bitmaps: A >= 32 -> wave w moves rows 64 (w & 1) + lane of block (w >> 1)'s word
   // column; A = 16 -> wave w moves all 128 rows of segment w's word column
   const uint32_t b_goff = A >= 32 ? (uint32_t)((64 * (w & 1) + lane) * wpr * 4) : (uint32_t)(lane * 4);
+  // The previous partial (2-byte types, rows in index order or through the closed-form
+  // basis) is DMAed into the K ring at the end of the list: rows 0..63 of the block while
+  // the last iteration runs, rows 64..127 at the last step; 16-row segments as for K.
+  const bool prev16 = a.prev_o && a.prev_dtype != PA_F32;
+  const bool prev_dma = prev16 && !(a.scatter_o && has_pq && !closed);
+  const bool prev_closed = a.scatter_o && closed;
+  const uint32_t p_goff =
+      (uint32_t)(rs * (prev_closed ? a.residue_s : 1)) * (uint32_t)(a.prev_sn * 2) + 16u * (uint32_t)(pu ^ rs);
+  const char* pbase = a.prev_o + bh * a.prev_sb * 2;
 
   // ---- LDS read geometry (loop invariant; slot / block / chunk offsets are immediates)
   // QK: lane (m, G) reads K row 32 lb + m, unit 2 kc + G.
@@ -235,6 +245,16 @@ void attn_stream_kernel(const AttnK a) {
     _Pragma("unroll") for (int t = 0; t < 4; ++t)                                                 \
       dma_x4(lds0 + kVring + (SL) * kSlot + (16 * t + 4 * w) * 256,                               \
              vbase + (uint32_t)PA_SEG_ROW(dd, t) * vrow_b32, v_goff);                             \
+  } while (0)
+
+  // DMA of rows 64 h .. 64 h + 63 of the previous partial into K slot SL.
+#define PA_DMA_PREV(h, SL)                                                                        \
+  do {                                                                                            \
+    _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                               \
+      const int r_ = qb * 128 + 64 * (h) + 16 * t;                                                \
+      const int pr_ = prev_closed ? (r_ & rmask) * a.residue_s + (r_ >> a.residue_qlog2) : r_;    \
+      dma_x4(lds0 + kKring + (SL) * kSlot + (16 * t + 4 * w) * 256, pbase + (int64_t)pr_ * a.prev_sn * 2, p_goff); \
+    }                                                                                             \
   } while (0)
 
   // QK of both blocks of the step in K slot SL: 4 K reads ahead, then one read per MFMA
@@ -379,7 +399,10 @@ void attn_stream_kernel(const AttnK a) {
   do {                                                                                            \
     dma_wait_all();                                                                               \
     __syncthreads();                                                                              \
-    if ((jj) + 2 < n_steps) PA_DMA_K(d_j2, (P));                                                  \
+    if ((jj) + 2 < n_steps)                                                                       \
+      PA_DMA_K(d_j2, (P));                                                                        \
+    else if (prev_dma)                                                                            \
+      PA_DMA_PREV(0, (P));                                                                        \
     PA_DMA_V(d_j1, (P) ^ 1);                                                                      \
     StepDesc d_j3{};                                                                              \
     if ((jj) + 3 < n_steps) d_j3 = load_desc((jj) + 3);                                           \
@@ -421,7 +444,13 @@ void attn_stream_kernel(const AttnK a) {
   do {                                                                                            \
     dma_wait_all();                                                                               \
     __syncthreads();                                                                              \
-    PA_PREV_LOAD();                                                                               \
+    if (prev_dma) {                                                                               \
+      if (n_steps == 1) PA_DMA_PREV(0, (P) ^ 1);                                                  \
+      PA_DMA_PREV(1, (P));                                                                        \
+      if (a.prev_o) prev_lse = a.prev_lse[bh * a.lse_sb + srow];                                  \
+    } else {                                                                                      \
+      PA_PREV_LOAD();                                                                             \
+    }                                                                                             \
     if (fc.live) {                                                                                \
       const float neg_m = -m_run;                                                                 \
       Frag pf00, pf01, pf10, pf11;                                                                \
@@ -439,7 +468,6 @@ void attn_stream_kernel(const AttnK a) {
   // Rows of the previous partial (prev_o, 2-byte types): 4 elements per (db, i4), the
   // columns this lane writes in the epilogue.
   const int srow = (a.scatter_o && has_pq) ? q_orig : r_idx;
-  const bool prev16 = a.prev_o && a.prev_dtype != PA_F32;
   uint2 prevw[NDB * 4];
   float prev_lse = -INFINITY;
 #define PA_PREV_LOAD()                                                                            \
@@ -496,6 +524,16 @@ void attn_stream_kernel(const AttnK a) {
       PA_LAST(1);
     else
       PA_LAST(0);
+    if (prev_dma) {
+      // rows 0..63 sit in K slot P ^ 1, rows 64..127 in slot P (P = parity of the last step)
+      dma_wait_all();
+      __syncthreads();
+      const int rr = (w & 1) * 32 + m;
+      lds_cptr prow_l = lds + kKring + ((j & 1) ^ ((w >> 1) ^ 1)) * kSlot + rr * 256 + 8 * G;
+#pragma unroll
+      for (int q_ = 0; q_ < NDB * 4; ++q_)
+        prevw[q_] = __builtin_bit_cast(uint2, *(const __attribute__((address_space(3))) u32x2*)(prow_l + 16 * (q_ ^ (rr & 15))));
+    }
   } else {
     PA_PREV_LOAD();
   }
@@ -514,6 +552,7 @@ void attn_stream_kernel(const AttnK a) {
 #undef PA_QK
 #undef PA_DMA_V
 #undef PA_DMA_K
+#undef PA_DMA_PREV
 #undef PA_SEG_ROW
 
   // ---- epilogue (as attn_fwd_kernel) -------------------------------------------
