@@ -98,6 +98,7 @@ struct Mma<__bf16> {
   __device__ static void store4(char* p, f32x4 x) {
     *reinterpret_cast<bf16x4*>(p) = __builtin_convertvector(x, bf16x4);
   }
+  __device__ static bf16x4 cvt4(f32x4 x) { return __builtin_convertvector(x, bf16x4); }
 };
 
 template <>
@@ -110,6 +111,7 @@ struct Mma<_Float16> {
   __device__ static void store4(char* p, f32x4 x) {
     *reinterpret_cast<f16x4*>(p) = __builtin_convertvector(x, f16x4);
   }
+  __device__ static f16x4 cvt4(f32x4 x) { return __builtin_convertvector(x, f16x4); }
 };
 
 template <>

@@ -577,7 +577,11 @@ void attn_stream_kernel(const AttnK a) {
       lse_v = M + logf(den);
     }
   }
-  char* orow = a.o + (bh * a.o_sb + (int64_t)srow * a.o_sn) * ESZ;
+  // The output rows go through LDS (the V ring, 8 KB per wave, swizzled as K) and leave as
+  // whole rows: 16 bytes per lane, four full rows per store instruction.
+  __syncthreads();  // every wave is past its last read of the V ring
+  lds_char_t* stage = (lds_char_t*)smem + kVring + w * 8192;
+  typedef __attribute__((address_space(3))) u32x2 lds_w2;
   const int psz = a.prev_dtype == PA_F32 ? 4 : 2;
   const char* prow = a.prev_o ? a.prev_o + (bh * a.prev_sb + (int64_t)srow * a.prev_sn) * psz : nullptr;
 #pragma unroll
@@ -598,10 +602,22 @@ void attn_stream_kernel(const AttnK a) {
           x += a_prev * load4_any(prow + d0 * psz, a.prev_dtype);
         }
       }
-      Mma<T>::store4(orow + d0 * ESZ, x);
+      *(lds_w2*)(stage + m * 256 + 16 * ((4 * db + i4) ^ (m & 15)) + 8 * G) =
+          __builtin_bit_cast(u32x2, Mma<T>::cvt4(x));
     }
   }
   if (a.lse && G == 0) a.lse[bh * a.lse_sb + srow] = lse_v;
+  // (each wave reads back only the rows it wrote: LDS keeps a wave's accesses in order)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = 4 * i + (lane >> 4);
+    const u32x4 v = *(lds_u4*)(stage + rr * 256 + 16 * ((lane & 15) ^ (rr & 15)));
+    const int r_ = qb * 128 + w * 32 + rr;
+    const int s_ = (a.scatter_o && has_pq)
+                       ? (closed ? (r_ & rmask) * a.residue_s + (r_ >> a.residue_qlog2) : a.pred.perm_q[r_])
+                       : r_;
+    *reinterpret_cast<u32x4*>(a.o + (bh * a.o_sb + (int64_t)s_ * a.o_sn) * ESZ + 16 * (lane & 15)) = v;
+  }
 }
 
 }  // namespace pa
