@@ -100,9 +100,11 @@ void attn_stream_kernel(const AttnK a) {
   const int G = lane >> 5;
   const int m = lane & 31;
 
-  const int64_t lid = xcd_remap(blockIdx.x, a.total_wg);
-  const int64_t bh = a.heads_desc ? a.BH - 1 - lid / a.nq : lid / a.nq;
-  const int qb_lin = (int)(lid % a.nq);
+  // (32-bit index arithmetic: the grid is below 2^31 work-groups, checked on the host)
+  const uint32_t lid = xcd_remap32(blockIdx.x, (uint32_t)a.total_wg);
+  const uint32_t bh_l = lid / (uint32_t)a.nq;
+  const int64_t bh = a.heads_desc ? a.BH - 1 - bh_l : bh_l;
+  const int qb_lin = (int)(lid - bh_l * (uint32_t)a.nq);
   const int qb = a.qblock_order ? a.qblock_order[qb_lin] : qb_lin;
   const int A = a.A;
   const int n_steps = (a.kv_num[qb] * A + 63) >> 6;

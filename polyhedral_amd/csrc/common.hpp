@@ -137,5 +137,12 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t hw, int64_t total) {
   // tail round (r == per): only XCDs x < rem exist here
   return x * per + x + per;
 }
+// The same in 32-bit arithmetic (total < 2^31).
+__device__ __forceinline__ uint32_t xcd_remap32(uint32_t hw, uint32_t total) {
+  const uint32_t per = total >> 3, rem = total & 7u;
+  const uint32_t x = hw & 7u, r = hw >> 3;
+  if (r < per) return x * per + (x < rem ? x : rem) + r;
+  return x * per + x + per;
+}
 
 }  // namespace pa
