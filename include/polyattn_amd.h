@@ -110,8 +110,9 @@ int pa_index_bits(const pa_mask* mask, int64_t N, int32_t BQ, int32_t A, const i
 /* Step descriptors of the streaming attention kernel (no counterpart in the reference:
  * a re-layout of the lists above).  The kernel consumes a query block's list as steps of
  * 64 kv columns = 4 segments of 16 columns (segment s of the list is column 16 (s mod
- * A/16) of listed tile s div (A/16)).  For query block i and step j, 16 int32 words at
- * steps[(i * steps_pitch + j) * 16]:
+ * A/16) of listed tile s div (A/16)).  Lists are written in issue order: list p holds
+ * query block i = order[p] (i = p when order is NULL), and its step j is 16 int32 words
+ * at steps[(p * steps_pitch + j) * 16]:
  *   [0..3]  K / V row of segment t's first column: the index-space column b, or with
  *           residue_s > 0 its original row (b mod 2^residue_qlog2) * residue_s +
  *           b div 2^residue_qlog2; 0 past the list (that segment's code is 0)
@@ -120,15 +121,17 @@ int pa_index_bits(const pa_mask* mask, int64_t N, int32_t BQ, int32_t A, const i
  *           from kv_partial when that is NULL: 0x55 partial, 0xff full)
  *   [5..8]  pool word offset of the bitmap word holding segment t's columns
  *           (kv_bits_off + (16 (s mod A/16)) / 32), -1 when the tile has no bitmap
- *   [9..14] zero
+ *   [9..12] zero
+ *   [13]    i, the query block of the list
+ *   [14]    the list's number of steps, ceil(kv_num[i] * A / 64)
  *   [15]    residue_s (0 for rows in index space)
  * steps_pitch >= ceil(pitch * A / 64).  kv_wave_bits and kv_bits_off may be NULL.
  * A launch that gathers K / V through the residue basis (gather_kv, residue_s) needs
  * steps built with the same residue_s; any other launch needs residue_s = 0. */
 int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
                    const uint32_t* kv_wave_bits, const int32_t* kv_bits_off, int64_t pitch, int64_t N,
-                   int32_t BQ, int32_t A, int32_t residue_s, int32_t residue_qlog2, int32_t* steps,
-                   int64_t steps_pitch, void* stream);
+                   int32_t BQ, int32_t A, int32_t residue_s, int32_t residue_qlog2, const int32_t* order,
+                   int32_t* steps, int64_t steps_pitch, void* stream);
 
 /* ---- class-A permutation (replaces gpu/permute.py:12-31) -------------------------
  * Row gather dst[b, p, :] = src[b, perm[p], :] (inverse = 0), the index_select of
@@ -180,9 +183,11 @@ typedef struct pa_attn_args {
   int64_t prev_sb, prev_sn;
   const float* prev_lse;   /* [BH, N] stride lse_sb, required with prev_o */
   const int32_t* qblock_order; /* NULL or [N/BQ] permutation: order query blocks are issued */
-  const int32_t* kv_steps;     /* NULL or pa_index_steps output for this index: enables the     */
-  int64_t steps_pitch;         /*   streaming kernel (f16/bf16, D = 128, BQ = 128, A in 16, 32, */
-                               /*   64, bitmaps for the partial tiles, no table gather of K/V)  */
+  const int32_t* kv_steps;     /* NULL or pa_index_steps output for this index, written in the */
+  int64_t steps_pitch;         /*   order of qblock_order: enables the streaming kernel (f16 /  */
+                               /*   bf16, D = 128, BQ = 128, A in 16, 32, 64, bitmaps for the   */
+                               /*   partial tiles, no table gather of K/V), which takes each    */
+                               /*   list's query block and length from its first descriptor    */
   int32_t heads_desc;          /* nonzero: heads are issued from the last to the first.  A pass */
                                /*   that follows another over the same tensors then starts on   */
                                /*   the heads the previous one touched last (still in cache).   */

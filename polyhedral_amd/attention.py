@@ -136,11 +136,18 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
     # the K / V rows of the step descriptors are in the basis K / V are gathered through
     steps_basis = int(residue) if (gather_kv and residue) else 0
     if kernel != "general" and (kv_bits is None or kv_steps is None):
-        reg_bits, reg_steps = stream_arrays_for(kv_idx, BQ, A, steps_basis)
+        reg_bits, reg_steps = stream_arrays_for(kv_idx, BQ, A, steps_basis, qblock_order)
         if kv_bits is None and kv_steps is None:
             kv_bits = reg_bits
         if kv_steps is None and (kv_bits is reg_bits or kv_bits is None):
             kv_steps = reg_steps
+    if kv_steps is not None and getattr(kv_steps, "order", None) is not qblock_order:
+        # the streaming kernel reads its lists in issue order: descriptors laid out for
+        # another order are rebuilt for this one from the registered index
+        _, kv_steps = stream_arrays_for(kv_idx, BQ, A, steps_basis, qblock_order)
+        if kv_steps is None:
+            raise ValueError("kv_steps were laid out for another qblock_order (build them with "
+                             "build_steps(..., order=qblock_order))")
     if kv_steps is not None and getattr(kv_steps, "residue_s", steps_basis) != steps_basis:
         raise ValueError(f"kv_steps hold K/V rows in the residue-{kv_steps.residue_s} basis; this call gathers "
                          f"in the residue-{steps_basis} basis (build them with build_steps(..., residue))")

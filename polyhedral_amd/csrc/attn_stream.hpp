@@ -105,10 +105,13 @@ void attn_stream_kernel(const AttnK a) {
   const uint32_t bh_l = lid / (uint32_t)a.nq;
   const int64_t bh = a.heads_desc ? a.BH - 1 - bh_l : bh_l;
   const int qb_lin = (int)(lid - bh_l * (uint32_t)a.nq);
-  const int qb = a.qblock_order ? a.qblock_order[qb_lin] : qb_lin;
+  // The lists are laid out in issue order; a list's first descriptor names its query
+  // block and its length, so one scalar load starts the work-group.
+  const StepDesc* desc = reinterpret_cast<const StepDesc*>(a.steps) + (int64_t)qb_lin * a.steps_pitch;
+  typedef const __attribute__((address_space(4))) int32_t cint;
+  const int qb = ((cint*)desc)[13];
+  const int n_steps = ((cint*)desc)[14];
   const int A = a.A;
-  const int n_steps = (a.kv_num[qb] * A + 63) >> 6;
-  const StepDesc* desc = reinterpret_cast<const StepDesc*>(a.steps) + (int64_t)qb * a.steps_pitch;
 
   const bool closed = a.residue_s != 0;
   const int32_t rmask = (1 << a.residue_qlog2) - 1;
@@ -194,7 +197,6 @@ void attn_stream_kernel(const AttnK a) {
   // them, and that lets the compiler use scalar loads (a vector load would be counted
   // in vmcnt together with the DMA and make the compiler's waits cover it).
   auto load_desc = [&](int jd) __attribute__((always_inline)) -> StepDesc {
-    typedef const __attribute__((address_space(4))) int32_t cint;
     cint* c = (cint*)(reinterpret_cast<const int32_t*>(desc + jd));
     StepDesc r{};
     r.base[0] = c[0];

@@ -294,11 +294,12 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(const int32_t* __restri
                                                           const uint32_t* __restrict__ kv_wave_bits,
                                                           const int32_t* __restrict__ kv_bits_off, int64_t pitch,
                                                           int32_t nq, int32_t BQ, int32_t A, int32_t residue_s,
-                                                          int32_t residue_qlog2, int32_t* __restrict__ steps,
-                                                          int64_t steps_pitch) {
+                                                          int32_t residue_qlog2, const int32_t* __restrict__ order,
+                                                          int32_t* __restrict__ steps, int64_t steps_pitch) {
   const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (gid >= (int64_t)nq * steps_pitch) return;
-  const int qb = (int)(gid / steps_pitch);
+  const int pos = (int)(gid / steps_pitch);  // issue position of the list
+  const int qb = order ? order[pos] : pos;
   const int j = (int)(gid % steps_pitch);
   const int spt = A >> 4;                    // 16-column segments per tile
   const int n_seg = kv_num[qb] * spt;
@@ -335,6 +336,8 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(const int32_t* __restri
     code |= c8 << (8 * t);
   }
   d[4] = (int32_t)code;
+  d[13] = qb;
+  d[14] = (kv_num[qb] * A + 63) >> 6;
   d[15] = residue_s > 0 ? residue_s : 0;
   int4* dst = reinterpret_cast<int4*>(steps + gid * 16);
 #pragma unroll
@@ -346,8 +349,8 @@ __global__ __launch_bounds__(kThreads) void steps_kernel(const int32_t* __restri
 
 extern "C" int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
                               const uint32_t* kv_wave_bits, const int32_t* kv_bits_off, int64_t pitch, int64_t N,
-                              int32_t BQ, int32_t A, int32_t residue_s, int32_t residue_qlog2, int32_t* steps,
-                              int64_t steps_pitch, void* stream) {
+                              int32_t BQ, int32_t A, int32_t residue_s, int32_t residue_qlog2,
+                              const int32_t* order, int32_t* steps, int64_t steps_pitch, void* stream) {
   PA_CHECK_ARG(kv_num, "pa_index_steps: null kv_num");
   PA_CHECK_ARG(N >= 1 && N <= (1ll << 30), "pa_index_steps: N=%lld out of range", (long long)N);
   PA_CHECK_ARG(pa::tile_ok(BQ) && pa::tile_ok(A) && N % BQ == 0 && N % A == 0,
@@ -370,7 +373,7 @@ extern "C" int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, cons
   hipLaunchKernelGGL(pa::steps_kernel, dim3((unsigned)((total + pa::kThreads - 1) / pa::kThreads)),
                      dim3(pa::kThreads), 0, static_cast<hipStream_t>(stream), kv_idx, kv_num, kv_partial,
                      kv_wave_bits, kv_bits_off, pitch, (int32_t)nq, BQ, A, residue_s > 0 ? residue_s : 0,
-                     residue_qlog2, steps, steps_pitch);
+                     residue_qlog2, order, steps, steps_pitch);
   PA_LAUNCH_CHECK("steps_kernel");
   return PA_OK;
 }

@@ -58,11 +58,13 @@ def _extras(kv_idx, BQ, A):
     return entry[1]
 
 
-def build_steps(kv_idx, kv_num, kv_partial, wave, bits_off, N, BQ, A, residue=0):
+def build_steps(kv_idx, kv_num, kv_partial, wave, bits_off, N, BQ, A, residue=0, order=None):
     """Step descriptors [N/BQ, ceil(pitch * A / 64), 16] int32 (pa_index_steps) whose
     K / V rows are in the residue-s basis (residue > 0, N / s a power of two) or in index
-    space (residue = 0); None for an index whose every list is empty.  The tensor carries
-    the basis as attribute ``residue_s``."""
+    space (residue = 0); None for an index whose every list is empty.  The lists are laid
+    out in the issue order ``order`` (int32 [N/BQ] device tensor, the qblock_order of the
+    launches that use them; None: index order).  The tensor carries the basis and the order
+    as attributes ``residue_s`` and ``order``."""
     nq, pitch = kv_idx.shape
     sp = (pitch * A + 63) // 64
     if sp == 0:
@@ -77,8 +79,10 @@ def build_steps(kv_idx, kv_num, kv_partial, wave, bits_off, N, BQ, A, residue=0)
     with torch.cuda.device(kv_idx.device):
         _lib.check(_lib.lib().pa_index_steps(_lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial),
                                              _lib.ptr(wave), _lib.ptr(bits_off), pitch, N, BQ, A, int(residue),
-                                             qlog2, _lib.ptr(steps), sp, _lib.stream_of(steps)), "pa_index_steps")
+                                             qlog2, _lib.ptr(order), _lib.ptr(steps), sp, _lib.stream_of(steps)),
+                   "pa_index_steps")
     steps.residue_s = int(residue)
+    steps.order = order
     return steps
 
 
@@ -158,7 +162,7 @@ def build_device(mask, N, BQ, A, *, perm=None, perm_kv=None, device=None, bits=F
                                        _lib.ptr(kv_partial), max_kv, _lib.ptr(part_base), _lib.ptr(off),
                                        _lib.ptr(pool), stream), "pa_index_bits")
             out = out + ((off, pool),)
-            _register(kv_idx, BQ, A, bits=(off, pool))
+            _register(kv_idx, BQ, A, bits=(off, pool), N=N, arrays=(kv_num, kv_partial, wave))
         if steps:
             st = build_steps(kv_idx, kv_num, kv_partial, wave, out[6][0], N, BQ, A, residue)
             out = out + (st,)
@@ -199,17 +203,25 @@ def wave_bits_for(kv_idx, BQ, A):
     return wave if wave is not None and wave.shape == kv_idx.shape else None
 
 
-def stream_arrays_for(kv_idx, BQ, A, residue=0):
-    """(bitmaps, step descriptors in the residue basis) registered for this kv_idx tensor,
-    building the descriptors for a new basis from the registered index arrays; (None,
-    None) when the index was not built with bitmaps."""
+def stream_arrays_for(kv_idx, BQ, A, residue=0, order=None):
+    """(bitmaps, step descriptors in the residue basis and the issue order ``order``)
+    registered for this kv_idx tensor, building the descriptors for a new basis or order
+    from the registered index arrays; (None, None) when the index was not built with
+    bitmaps."""
     ex = _extras(kv_idx, BQ, A)
     bits = ex.get("bits")
     if bits is None:
         return None, None
-    steps = ex["steps"].get(int(residue))
+    if order is None:
+        steps = ex["steps"].get(int(residue))
+    else:
+        hit = ex.setdefault("ordered", {}).get((int(residue), id(order)))
+        steps = hit[1] if hit is not None and hit[0] is order else None
     if steps is None and "arrays" in ex:
         kv_num, kv_partial, wave = ex["arrays"]
-        steps = build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], ex["N"], BQ, A, residue)
-        ex["steps"][int(residue)] = steps
+        steps = build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], ex["N"], BQ, A, residue, order)
+        if order is None:
+            ex["steps"][int(residue)] = steps
+        else:
+            ex["ordered"][(int(residue), id(order))] = (order, steps)
     return bits, steps

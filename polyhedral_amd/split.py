@@ -26,7 +26,7 @@ import torch
 
 from . import _lib
 from .attention import prepare
-from .index import STREAM_TILES, build_device
+from .index import STREAM_TILES, build_device, build_steps
 from .perm import residue_perm
 from .polyattn.masks import Permuted
 from .spec import MaskSpec
@@ -68,14 +68,15 @@ class SplitPlan:
                           else torch.from_numpy(np.asarray(p.perm, dtype=np.int32)).to(dev))
             mask = Permuted(p.mask, perm_t.cpu().numpy()) if perm_t is not None else p.mask
             stream = (p.BQ, p.A) in STREAM_TILES
-            built = build_device(mask, N, p.BQ, p.A, device=dev, bits=True, steps=stream,
-                                 residue=_closed_form_residue(p, N))
+            built = build_device(mask, N, p.BQ, p.A, device=dev, bits=True)
             kv_idx, kv_num, kv_partial, wave, tiles, live, bits = built[:7]
-            steps = built[7] if stream else None
             inc, exc = p.mask.terms()
             # longest-processing-time first: query blocks with the most listed tiles are
             # issued first, so the tail of the grid is short blocks
             qorder = torch.argsort(kv_num, descending=True, stable=True).to(torch.int32) if order == "lpt" else None
+            # the streaming kernel's descriptors, laid out in that issue order
+            steps = (build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], N, p.BQ, p.A,
+                                 _closed_form_residue(p, N), qorder) if stream else None)
             self.built.append(dict(piece=p, spec=MaskSpec(tuple(inc), tuple(exc)), perm=perm_t,
                                    kv_idx=kv_idx, kv_num=kv_num, kv_partial=kv_partial, wave=wave, bits=bits,
                                    steps=steps,

@@ -20,7 +20,7 @@ STREAM_MASKS = ["window-128", "causal", "dilated-8", "local256+str8", "twoband-1
                 "prefixlm-2048", "lat16-band256"]
 
 
-def _expected_steps(kv_idx, kv_num, wave, bits_off, BQ, A, N=0, residue=0):
+def _expected_steps(kv_idx, kv_num, wave, bits_off, BQ, A, N=0, residue=0, order=None):
     """The descriptor layout of include/polyattn_amd.h (pa_index_steps), from the index."""
     nq, pitch = kv_idx.shape
     spt = A // 16
@@ -28,7 +28,8 @@ def _expected_steps(kv_idx, kv_num, wave, bits_off, BQ, A, N=0, residue=0):
     ngr = max(1, BQ // 32)
     sp = (pitch * A + 63) // 64
     out = np.zeros((nq, sp, 16), dtype=np.int64)
-    for qb in range(nq):
+    for pos in range(nq):
+        qb = int(order[pos]) if order is not None else pos
         n_seg = int(kv_num[qb]) * spt
         for j in range(sp):
             code = 0
@@ -47,11 +48,13 @@ def _expected_steps(kv_idx, kv_num, wave, bits_off, BQ, A, N=0, residue=0):
                         c8 |= ((wb >> (2 * (g * ncg + cg))) & 3) << (2 * g)
                     if bits_off[qb, ti] >= 0:
                         boff = int(bits_off[qb, ti]) + ((within * 16) >> 5)
-                out[qb, j, t] = base
-                out[qb, j, 5 + t] = boff
+                out[pos, j, t] = base
+                out[pos, j, 5 + t] = boff
                 code |= c8 << (8 * t)
-            out[qb, j, 4] = code
-            out[qb, j, 15] = residue
+            out[pos, j, 4] = code
+            out[pos, j, 13] = qb
+            out[pos, j, 14] = (int(kv_num[qb]) * A + 63) // 64
+            out[pos, j, 15] = residue
     return (out & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
 
 
@@ -68,6 +71,13 @@ def test_step_descriptors_follow_the_index(gpu, name, A, residue):
     got = steps.cpu().numpy()
     assert got.shape == want.shape
     assert np.array_equal(got, want), f"{name} A={A}: first mismatch at {np.argwhere(got != want)[:3]}"
+    # laid out in an issue order (a fixed permutation of the query blocks)
+    order = torch.from_numpy(np.random.default_rng(A).permutation(N // BQ).astype(np.int32)).to(gpu)
+    st2 = pindex.build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], N, BQ, A, residue, order)
+    assert st2.order is order
+    want2 = _expected_steps(kv_idx.cpu().numpy(), kv_num.cpu().numpy(), wave.cpu().numpy(),
+                            bits[0].cpu().numpy(), BQ, A, N, residue, order.cpu().numpy())
+    assert np.array_equal(st2.cpu().numpy(), want2), f"{name} A={A} ordered"
 
 
 def _launch(q, k, v, bi, name, BQ, A, kernel, **kw):
@@ -90,6 +100,19 @@ def test_stream_kernel_equals_oracle(gpu, name, dtype, A):
     launch, out = _launch(qd, kd, vd, bi, name, BQ, A, "stream")
     assert launch.kernel == "stream"
     check_close(out, want, dtype, f"stream {name} {dtype} 128x{A}")
+
+
+@pytest.mark.parametrize("name", ["lat16-band256", "sinks4+win256"])
+def test_stream_with_issue_order(gpu, name):
+    """Lists issued in a permuted order (the descriptors are rebuilt for that order)."""
+    N, D, BQ, A = 2048, 128, 128, 32
+    q, k, v = make_qkv(2, N, D, torch.bfloat16, seed=11)
+    want, _ = oatt.dense_attention(as64(q), as64(k), as64(v), oatt.spec_rows(om.NAMED[name], N))
+    bi = pindex.build(numpy_mask(name), N, BQ, A)
+    order = torch.from_numpy(np.random.default_rng(3).permutation(N // BQ).astype(np.int32)).to(gpu)
+    launch, out = _launch(q.to(gpu), k.to(gpu), v.to(gpu), bi, name, BQ, A, "stream", qblock_order=order)
+    assert launch.kernel == "stream"
+    check_close(out, want, torch.bfloat16, f"stream {name} ordered")
 
 
 def test_auto_selects_each_kernel(gpu):
