@@ -65,6 +65,30 @@ def measure(plan_launches, steps, warmup):
     return wall_ms, per
 
 
+def measure_isolated(plan_launches, reps, flush_mib=512):
+    """The reference's timing protocol (gpu/bench.py:11-24), with the flush sized for this
+    GPU: before each forward a flush_mib MiB buffer is zeroed (more than the 256 MiB
+    memory-side cache), then one forward is timed alone with events and the device is
+    synchronised.  Returns the median in ms."""
+    import statistics
+
+    import torch
+    dev = plan_launches[0].device
+    cache = torch.empty(flush_mib * (1 << 20) // 4, dtype=torch.int32, device=dev)
+    out = []
+    for _ in range(reps):
+        cache.zero_()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for launch in plan_launches:
+            launch()
+        e.record()
+        torch.cuda.synchronize()
+        out.append(s.elapsed_time(e))
+    del cache
+    return statistics.median(out)
+
+
 def cpu_baseline(wl, budget_s=12.0):
     """Oracle dense fp32 attention on the host over (head, 1024-row chunk) units in
     order until the budget is spent; live-FLOP TFLOP/s over what was processed."""
@@ -123,6 +147,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     q, k, v = wl.inputs(0, dev)
     launches, o, lse = plan.prepare(q, k, v)
     wall_ms, per_launch = measure(launches, steps, warmup)
+    iso_ms = measure_isolated(launches, max(25, min(steps, 100)))
     kernels = ["attn_stream_kernel" if x.kernel == "stream" else "attn_fwd_kernel" for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
     for i, bi in enumerate(plan.launched):
@@ -151,6 +176,10 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
         min_hbm_bytes=4 * wl.H * wl.L * wl.D * q.element_size(),
     )
     res["hbm_floor_ms"] = round(res["min_hbm_bytes"] / (HBM_GBPS * 1e9) * 1e3, 5)
+    res["isolated"] = dict(ms_median=round(iso_ms, 5), live_tflops=round(flops_live / (iso_ms * 1e-3) / 1e12, 3),
+                           protocol="one forward per event pair after zeroing a 512 MiB buffer, device synchronised "
+                                    "between forwards, median (gpu/bench.py:11-24 with a flush larger than the "
+                                    "memory-side cache)")
     res["_launches"] = len(launches)
     if with_cpu:
         log(f"[bench] cpu baseline for {name} ...")
@@ -204,7 +233,8 @@ def main():
                 r = rows[-1]
                 log(f"[bench]   {r['ms_per_step']:.4f} ms/step  kernel {r['kernel_ms']:.4f} ms  "
                     f"{r['kernel_live_tflops']:.1f} live TFLOP/s ({100 * r['frac_peak']:.1f}% of {r['peak_tflops']})"
-                    f"  waste {r['waste']}")
+                    f"  waste {r['waste']}  isolated {r['isolated']['ms_median']:.4f} ms "
+                    f"({r['isolated']['live_tflops']:.1f} TFLOP/s)")
         out = dict(device=torch.cuda.get_device_name(0), results=rows)
         if a.report:
             with open(a.report, "w") as f:
@@ -229,6 +259,7 @@ def main():
                              " (all launches of one step)",
                       algorithmic="live FLOP = 4 * D * live pairs * heads per launch"),
         cpu_baseline=r.get("cpu_baseline"),
+        isolated=r["isolated"],
     )
     print(json.dumps(line), flush=True)
 

@@ -192,6 +192,17 @@ typedef struct pa_attn_args {
                                /*   that follows another over the same tensors then starts on   */
                                /*   the heads the previous one touched last (still in cache).   */
                                /*   Results do not depend on it.                                */
+  /* Class-B traffic emulation (gpu/triton_attn.py:99-128, 202-205).  gather_mult > 1: for
+   * every listed tile the K rows are read as sum_r wsel[b * wsel_sb + r] * K[row_r] over
+   * r < gather_mult, row_0 being the tile's row for kv column c and, for r >= 1,
+   * gather_scatter = 0: (row_0 + r A) mod N (contiguous extra rows), gather_scatter != 0:
+   * perm_kv((c + r A) mod N) (scattered).  wsel is [BH, gather_mult] in the dtype of q,
+   * [1, 0, ...] in the reference: the extra rows are read and the result is unchanged.
+   * General kernel only (not with kv_steps). */
+  int32_t gather_mult;    /* 0 or 1: off */
+  int32_t gather_scatter;
+  const void* wsel;
+  int64_t wsel_sb;
 } pa_attn_args;
 
 int pa_attn_fwd(const pa_attn_args* args, void* stream);

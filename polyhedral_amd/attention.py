@@ -13,8 +13,8 @@ gfx950 kernel) instead of the Triton JIT.  Differences a caller can observe:
 * num_warps / num_stages are Triton launch knobs; every (num_warps, num_stages) of
   gpu/launchsweep.py:15-16 is accepted and the HIP kernel's shape is fixed by
   (BQ, A, D, dtype), so there is no pipeliner fallback to take.
-* gather_mult > 1 (the class-B traffic emulation of gpu/triton_attn.py:109-128)
-  raises NotImplementedError.
+* gather_mult > 1 (the class-B traffic emulation of gpu/triton_attn.py:108-128)
+  runs on the general kernel (the streaming kernel does not emulate it).
 
 Keyword-only extensions: kv_wave_bits (per-wave skip codes; found automatically for
 an index made by blockindex.build / to_cuda), kv_bits (element bitmaps of the
@@ -98,7 +98,7 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
             perm_q=None, perm_kv=None, gather_kv=False, gather_mult=1, gather_scatter=True,
             num_warps=4, num_stages=2, *, kv_wave_bits=None, kv_bits=None, gather_q=False, scatter_o=False,
             residue=0, lse=None, prev=None, out=None, qblock_order=None, kv_steps=None, kernel="auto",
-            heads_desc=False):
+            heads_desc=False, wsel=None):
     """Validate the arguments of block_sparse_attention once and return a Launch.
 
     heads_desc: issue the heads from the last to the first (the results are the same; a
@@ -109,8 +109,9 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
     _assert_kinds_match()
     assert N % BQ == 0 and N % A == 0, "cost model and kernel both assume this"
     assert k.shape == v.shape == q.shape
-    if gather_mult != 1:
-        raise NotImplementedError("gather_mult > 1 (class-B traffic emulation) is not built")
+    if int(gather_mult) < 1:
+        raise ValueError(f"gather_mult={gather_mult} must be >= 1")
+    gather_mult = int(gather_mult)
     _lib.require_device(q, k, v, kv_idx, kv_num, kv_partial)
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _rows3(t, n)
@@ -220,7 +221,9 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
     # the streaming kernel's preconditions (pa_attn_fwd rejects kv_steps otherwise)
     pitch = kv_idx.shape[1]
     why = None
-    if q.dtype not in (torch.float16, torch.bfloat16) or D != 128 or (BQ, A) not in STREAM_TILES:
+    if gather_mult > 1:
+        why = "gather_mult > 1 (the class-B traffic emulation runs on the general kernel)"
+    elif q.dtype not in (torch.float16, torch.bfloat16) or D != 128 or (BQ, A) not in STREAM_TILES:
         why = f"dtype {q.dtype}, D={D}, tile {BQ}x{A} (needs f16/bf16, D=128, BQ=128, A in 16/32/64)"
     elif gathers_kv and not residue:
         why = "K/V gathered through a permutation table (only the closed-form residue basis)"
@@ -238,6 +241,19 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
             raise ValueError("kv_steps must be contiguous int32 [N/BQ, steps, 16]")
         args.kv_steps, args.steps_pitch = _lib.ptr(kv_steps), kv_steps.shape[1]
     args.heads_desc = 1 if heads_desc else 0
+    wsel_t = None
+    if gather_mult > 1:
+        # [1, 0, ...] per batch-head, as gpu/triton_attn.py:202-205: runtime weights keep the
+        # extra K reads alive and leave the result unchanged (wsel= overrides them)
+        if wsel is None:
+            wsel_t = torch.zeros(BH, gather_mult, dtype=q.dtype, device=dev)
+            wsel_t[:, 0] = 1
+        else:
+            wsel_t = wsel.to(device=dev, dtype=q.dtype).contiguous()
+            if wsel_t.shape != (BH, gather_mult):
+                raise ValueError(f"wsel must be [BH, gather_mult] = [{BH}, {gather_mult}]")
+        args.gather_mult, args.gather_scatter = gather_mult, 1 if gather_scatter else 0
+        args.wsel, args.wsel_sb = _lib.ptr(wsel_t), wsel_t.stride(0)
     keep = [q, k, v, o, kv_idx, kv_num, kv_partial, kv_wave_bits, kv_bits, dmask, lse, prev, qblock_order,
-            kv_steps]
+            kv_steps, wsel_t]
     return Launch(args, keep, o, dev, "stream" if use_stream else "general")

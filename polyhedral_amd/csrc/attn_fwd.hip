@@ -102,6 +102,15 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   a.steps_pitch = x->steps_pitch;
   a.BH = x->BH;
   a.heads_desc = x->heads_desc != 0;
+  a.gather_mult = x->gather_mult > 1 ? x->gather_mult : 1;
+  a.gather_scatter = x->gather_scatter != 0;
+  a.wsel = static_cast<const char*>(x->wsel);
+  a.wsel_sb = x->wsel_sb;
+  PA_CHECK_ARG(x->gather_mult <= 1 || (x->wsel && x->wsel_sb >= x->gather_mult),
+               "pa_attn_fwd: gather_mult=%d needs wsel [BH, >= gather_mult]", x->gather_mult);
+  PA_CHECK_ARG(x->gather_mult <= 1 || !x->kv_steps,
+               "pa_attn_fwd: gather_mult > 1 runs on the general kernel (pass no kv_steps)");
+  PA_CHECK_ARG(x->gather_mult <= 64, "pa_attn_fwd: gather_mult=%d too large", x->gather_mult);
   PA_CHECK_ARG(a.total_wg <= 0x7fffffffll, "pa_attn_fwd: %lld work-groups exceed the grid limit",
                (long long)a.total_wg);
 

@@ -78,6 +78,9 @@ struct AttnK {
   int64_t steps_pitch;
   int64_t BH;
   int32_t heads_desc;  // heads issued last to first
+  int32_t gather_mult, gather_scatter;  // class-B traffic emulation (K only)
+  const char* wsel;
+  int64_t wsel_sb;
 };
 
 constexpr int kStep = 64;          // KV rows per staged step
@@ -122,6 +125,33 @@ struct Mma<float> {
   }
   __device__ static void store4(char* p, f32x4 x) { *reinterpret_cast<f32x4*>(p) = x; }
 };
+
+// Class-B traffic emulation (gpu/triton_attn.py:108-128): one 16-byte unit of K rows
+// (row krow, kv column col) becomes sum_r wsel[r] * K[row_r] over r < gather_mult, the
+// extra rows read contiguously ((krow + r A) mod N) or through the kv permutation
+// (perm_kv((col + r A) mod N)).  Accumulated in fp32, rounded once.
+template <typename T>
+__device__ __forceinline__ uint4 gather_mult_unit(const AttnK& a, const char* kbase, int64_t krow_b, int64_t bh,
+                                                  uint4 kx, int krow, int col, int un16) {
+  constexpr int E = sizeof(T) == 4 ? 4 : 8;
+  typedef float fv __attribute__((ext_vector_type(E)));
+  typedef T tv __attribute__((ext_vector_type(E)));
+  const T* ws = reinterpret_cast<const T*>(a.wsel) + bh * a.wsel_sb;
+  const int32_t rmask = (1 << a.residue_qlog2) - 1;
+  fv acc = __builtin_convertvector(__builtin_bit_cast(tv, kx), fv) * (float)ws[0];
+  for (int r = 1; r < a.gather_mult; ++r) {
+    int er;
+    if (a.gather_scatter) {
+      const int c = (int)(((int64_t)col + (int64_t)r * a.A) % a.N);
+      er = a.residue_s ? (c & rmask) * a.residue_s + (c >> a.residue_qlog2) : (a.pred.perm_kv ? a.pred.perm_kv[c] : c);
+    } else {
+      er = (int)(((int64_t)krow + (int64_t)r * a.A) % a.N);
+    }
+    const uint4 x = *reinterpret_cast<const uint4*>(kbase + (int64_t)er * krow_b + un16);
+    acc += __builtin_convertvector(__builtin_bit_cast(tv, x), fv) * (float)ws[r];
+  }
+  return __builtin_bit_cast(uint4, __builtin_convertvector(acc, tv));
+}
 
 // 4 consecutive elements of a partial result in dtype dt, as floats.
 __device__ __forceinline__ f32x4 load4_any(const char* p, int32_t dt) {
@@ -354,10 +384,13 @@ _Pragma("unroll") \
         const char* vp = vbase + (int64_t)grow * vrow_b; \
         kx = *reinterpret_cast<const uint4*>(kp + (int)(rr * kstep_b) + t_un16); \
         vx = *reinterpret_cast<const uint4*>(vp + (int)(rr * vstep_b) + t_un16); \
+        if (a.gather_mult > 1 && valid) \
+          kx = gather_mult_unit<T>(a, kbase, krow_b, bh, kx, grow + rr * rstride, b0 + rr, t_un16); \
       } else { \
         const int lr = valid ? a.pred.perm_kv[b0 + rr] : 0; \
         kx = *reinterpret_cast<const uint4*>(kbase + (int64_t)lr * krow_b + t_un16); \
         vx = *reinterpret_cast<const uint4*>(vbase + (int64_t)lr * vrow_b + t_un16); \
+        if (a.gather_mult > 1 && valid) kx = gather_mult_unit<T>(a, kbase, krow_b, bh, kx, lr, b0 + rr, t_un16); \
       } \
       if (!valid) vx = uint4{0, 0, 0, 0}; \
       kreg[4 * i] = kx.x; kreg[4 * i + 1] = kx.y; kreg[4 * i + 2] = kx.z; kreg[4 * i + 3] = kx.w; \
