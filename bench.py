@@ -89,6 +89,46 @@ def measure_isolated(plan_launches, reps, flush_mib=512):
     return statistics.median(out)
 
 
+def measure_permute(q, k, v, s, reps=50, warmup=10):
+    """The class-A relabelling as standalone HBM gather / scatter kernels (the path of
+    gpu/permute.py:22-24 and gpu/exp5_amortisation.py, which the fused attention path does
+    not need): Q, K, V gathered through the residue-s permutation by one pa_permute_stack
+    launch, and O scattered back by pa_permute_rows.  Algorithmic bytes: each tensor
+    read once and written once."""
+    import torch
+
+    from polyhedral_amd import perm as pperm
+    N = q.shape[1]
+    p = pperm.residue_perm_device(N, s, q.device)
+    o = torch.empty_like(q)
+    ob = torch.empty_like(q)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(reps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / reps
+
+    ms_g = timed(lambda: pperm.permute_stack([q, k, v], p, with_positions=True))
+    ms_s = timed(lambda: pperm.permute_rows(o, p, inverse=True, out=ob))
+    tb = q.numel() * q.element_size()
+
+    def entry(ms, nbytes):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return dict(ms=round(ms, 5), bytes=nbytes, gb_per_s=round(gbs, 1),
+                    roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_GBPS, unit="GB/s",
+                                  frac=round(gbs / HBM_GBPS, 4)))
+    return dict(residue=s, gather_qkv=entry(ms_g, 3 * 2 * tb), scatter_o=entry(ms_s, 2 * tb),
+                note="algorithmic bytes = 2 x tensor bytes per tensor moved; gather_qkv is one "
+                     "pa_permute_stack launch (Q, K, V and the position ids), scatter_o one pa_permute_rows")
+
+
 def cpu_baseline(wl, budget_s=12.0):
     """Oracle dense fp32 attention on the host over (head, 1024-row chunk) units in
     order until the budget is spent; live-FLOP TFLOP/s over what was processed."""
@@ -148,6 +188,8 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     launches, o, lse = plan.prepare(q, k, v)
     wall_ms, per_launch = measure(launches, steps, warmup)
     iso_ms = measure_isolated(launches, max(25, min(steps, 100)))
+    residues = [b["piece"].residue for b in plan.built if b["piece"].residue]
+    permute = measure_permute(q, k, v, residues[0]) if residues and variant is None else None
     kernels = ["attn_stream_kernel" if x.kernel == "stream" else "attn_fwd_kernel" for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
     for i, bi in enumerate(plan.launched):
@@ -180,6 +222,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
                            protocol="one forward per event pair after zeroing a 512 MiB buffer, device synchronised "
                                     "between forwards, median (gpu/bench.py:11-24 with a flush larger than the "
                                     "memory-side cache)")
+    res["permute"] = permute
     res["_launches"] = len(launches)
     if with_cpu:
         log(f"[bench] cpu baseline for {name} ...")
@@ -235,6 +278,10 @@ def main():
                     f"{r['kernel_live_tflops']:.1f} live TFLOP/s ({100 * r['frac_peak']:.1f}% of {r['peak_tflops']})"
                     f"  waste {r['waste']}  isolated {r['isolated']['ms_median']:.4f} ms "
                     f"({r['isolated']['live_tflops']:.1f} TFLOP/s)")
+                if r.get("permute"):
+                    pm_ = r["permute"]
+                    log(f"[bench]   permute rp{pm_['residue']}: Q/K/V gather {pm_['gather_qkv']['gb_per_s']:.0f} GB/s, "
+                        f"O scatter {pm_['scatter_o']['gb_per_s']:.0f} GB/s")
         out = dict(device=torch.cuda.get_device_name(0), results=rows)
         if a.report:
             with open(a.report, "w") as f:
@@ -260,6 +307,7 @@ def main():
                       algorithmic="live FLOP = 4 * D * live pairs * heads per launch"),
         cpu_baseline=r.get("cpu_baseline"),
         isolated=r["isolated"],
+        permute=r["permute"],
     )
     print(json.dumps(line), flush=True)
 

@@ -142,6 +142,20 @@ int pa_permute_rows(const void* src, void* dst, const int32_t* perm, int64_t BH,
                     int64_t row_bytes, int64_t src_bh_stride, int64_t src_row_stride,
                     int64_t dst_bh_stride, int64_t dst_row_stride, int32_t inverse, void* stream);
 
+/* Once-per-forward relabelling of a stack of tensors (the regime of
+ * gpu/exp5_amortisation.py:89-118, where the stack runs in the permuted basis): one
+ * launch gathers (inverse = 0) or scatters (inverse = 1) the rows of n_tensors <= 8
+ * tensors of one shape and stride, as pa_permute_rows, and moves their position ids
+ * with them: pos_out[d] = pos_in[s] for each row moved from s to d (pos_in NULL: the ids
+ * are the source rows themselves, pos_out[p] = perm[p] for a gather), so that
+ * position-dependent ops (RoPE, gpu/exp5_amortisation.py:44-57) see every token's
+ * original position.  srcs / dsts are host arrays of device pointers; pos_in / pos_out
+ * are NULL or int64 [N] on the device (shared by every batch-head). */
+int pa_permute_stack(const void* const* srcs, void* const* dsts, int32_t n_tensors, const int32_t* perm,
+                     int64_t BH, int64_t N, int64_t row_bytes, int64_t src_bh_stride, int64_t src_row_stride,
+                     int64_t dst_bh_stride, int64_t dst_row_stride, const int64_t* pos_in, int64_t* pos_out,
+                     int32_t inverse, void* stream);
+
 /* inv[perm[p]] = p  (gpu/permute.py:27-31). */
 int pa_invert_perm(const int32_t* perm, int32_t* inv, int64_t N, void* stream);
 

@@ -57,6 +57,8 @@ SIGNATURES = {
                                       c_vp, c_i64, c_vp]),
     "pa_permute_rows": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                        c_i32, c_vp]),
+    "pa_permute_stack": (ctypes.c_int, [c_vp, c_vp, c_i32, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                        c_vp, c_vp, c_i32, c_vp]),
     "pa_invert_perm": (ctypes.c_int, [c_vp, c_vp, c_i64, c_vp]),
     "pa_residue_perm": (ctypes.c_int, [c_vp, c_i64, c_i32, c_vp]),
     "pa_attn_fwd": (ctypes.c_int, [ctypes.POINTER(PaAttnArgs), c_vp]),

@@ -50,6 +50,50 @@ def permute_rows(x, perm, inverse=False, out=None):
     return out
 
 
+def permute_stack(tensors, perm, positions=None, inverse=False, with_positions=True):
+    """One launch (pa_permute_stack): every tensor of `tensors` ([BH, N, ...], one shape)
+    gathered through perm (out[:, p] = x[:, perm[p]]; inverse=True scatters), and the
+    position ids moved with the tokens: pos_out[p] = positions[perm[p]] (positions None:
+    the original positions perm[p] themselves).  Returns (list of tensors, int64 [N]
+    positions or None).  The permuted stack then runs a whole forward in the permuted
+    basis, and position-dependent ops (RoPE) read pos_out instead of arange(N)
+    (gpu/exp5_amortisation.py:44-57, 89-118)."""
+    tensors = list(tensors)
+    if not 1 <= len(tensors) <= 8:
+        raise ValueError("permute_stack takes 1 to 8 tensors")
+    _lib.require_device(*tensors)
+    x0 = tensors[0]
+    if x0.dim() < 2:
+        raise ValueError("permute_stack expects [BH, N, ...] tensors")
+    xs = [x if (x.stride(-1) == 1 and x[0, 0].is_contiguous()) else x.contiguous() for x in tensors]
+    for x in xs[1:]:
+        if x.shape != x0.shape or x.dtype != x0.dtype or x.stride() != xs[0].stride() or x.device != x0.device:
+            raise ValueError("permute_stack tensors must share shape, dtype, strides and device")
+    BH, N = x0.shape[0], x0.shape[1]
+    p = _perm32(perm, x0.device)
+    if p.numel() != N:
+        raise ValueError(f"perm has {p.numel()} entries for {N} rows")
+    outs = [torch.empty_like(x, memory_format=torch.contiguous_format) for x in xs]
+    pos_in = None
+    if positions is not None:
+        pos_in = positions.to(device=x0.device, dtype=torch.int64).contiguous()
+        if pos_in.numel() != N:
+            raise ValueError(f"positions has {pos_in.numel()} entries for {N} rows")
+    pos_out = torch.empty(N, dtype=torch.int64, device=x0.device) if with_positions else None
+    esz = x0.element_size()
+    row_bytes = xs[0][0, 0].numel() * esz
+    n = len(xs)
+    srcs = (_lib.c_vp * n)(*[x.data_ptr() for x in xs])
+    dsts = (_lib.c_vp * n)(*[o.data_ptr() for o in outs])
+    with torch.cuda.device(x0.device):
+        _lib.check(_lib.lib().pa_permute_stack(srcs, dsts, n, _lib.ptr(p), BH, N, row_bytes,
+                                               xs[0].stride(0) * esz, xs[0].stride(1) * esz,
+                                               outs[0].stride(0) * esz, outs[0].stride(1) * esz,
+                                               _lib.ptr(pos_in), _lib.ptr(pos_out), int(inverse),
+                                               _lib.stream_of(x0)), "pa_permute_stack")
+    return outs, pos_out
+
+
 def apply_perm(x, perm):
     """gpu/permute.py:22-24: x [BH, N, D] -> rows reordered so position p holds original perm[p]."""
     return permute_rows(x, perm, inverse=False)
