@@ -126,7 +126,8 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
     PA_CHECK_ARG(!x->gather_kv || x->residue_s > 0,
                  "pa_attn_fwd: kv_steps supports gather_kv only through the closed-form residue basis");
     PA_CHECK_ARG(x->pitch == 0 || x->kv_bits, "pa_attn_fwd: kv_steps needs the partial-tile bitmaps");
-    PA_CHECK_ARG(x->steps_pitch >= (x->pitch * x->A + 63) / 64, "pa_attn_fwd: steps_pitch=%lld < %lld",
+    PA_CHECK_ARG(x->steps_pitch >= 1 && x->steps_pitch >= (x->pitch * x->A + 63) / 64,
+                 "pa_attn_fwd: steps_pitch=%lld < max(1, %lld) (every list's first descriptor is read)",
                  (long long)x->steps_pitch, (long long)((x->pitch * x->A + 63) / 64));
     PA_CHECK_ARG((reinterpret_cast<uintptr_t>(x->kv_steps) & 15) == 0, "pa_attn_fwd: kv_steps not 16-byte aligned");
     {
