@@ -229,6 +229,54 @@ int pa_lse_merge(const float* const* o_parts, const float* const* lse_parts, int
                  void* o, int32_t out_dtype, float* lse_out, int64_t BH, int64_t N, int32_t D,
                  void* stream);
 
+/* ---- decoding against a cache kept in a class-A basis ------------------------------
+ * The reference relabels tokens for prefill only and leaves decoding open: new keys
+ * arrive in original order and would have to be inserted at permuted positions
+ * (docs/NOTES.md:2145-2153, 2201-2203).  These entry points answer it for the residue
+ * bases of gpu/permute.py:12-15.  A cache of `capacity` rows per head (a multiple of
+ * s; s = residue_s, 0 or 1 = identity) keeps the token at original position t at row
+ * (t mod s) * (capacity / s) + t div s, so appending never moves a cached row.
+ *
+ * pa_kv_append: rows j = 0..n-1 of k_new / v_new [BH, n, D] (strides in elements) are
+ * the tokens at original positions pos0 + j; each is written to its basis row of
+ * k_cache / v_cache [BH, capacity, D].  pos0 + n <= capacity. */
+int pa_kv_append(const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sn, void* k_cache,
+                 void* v_cache, int64_t c_sb, int64_t c_sn, int64_t BH, int64_t n, int32_t D, int32_t dtype,
+                 int64_t capacity, int64_t pos0, int32_t residue_s, void* stream);
+
+/* pa_decode_fwd: o[b, i] = softmax over the cached tokens t < length that are live for
+ * the query at original position qpos0 + i under `mask` (perm_q / perm_kv NULL), of
+ * (q[b, i] . k_t) * scale, applied to v_t; a query with no live token gives 0 and lse
+ * -inf (gpu/reference.py:5-17 on one row).  1 <= nq <= 8; D = 64 or 128 (float32: 64);
+ * q, o [BH, nq, D], lse [BH, nq] fp32 or NULL; scale <= 0 means 1/sqrt(D).  The split
+ * partials go to `workspace`, whose size pa_decode_workspace returns for these
+ * arguments (it depends on BH, nq, D, capacity, length and residue_s).  A PA_DENSE
+ * mask must hold rows up to qpos0 + nq - 1. */
+typedef struct pa_decode_args {
+  const void* q;
+  int64_t q_sb, q_sn;
+  int32_t nq;
+  int64_t qpos0;
+  const void* k_cache;
+  const void* v_cache;
+  int64_t c_sb, c_sn;
+  int64_t capacity, length;
+  int32_t residue_s;
+  pa_mask mask;
+  int64_t BH;
+  int32_t D, dtype;
+  float scale;
+  void* o;
+  int64_t o_sb, o_sn;
+  float* lse;
+  int64_t lse_sb;
+  void* workspace;
+  int64_t workspace_bytes;
+} pa_decode_args;
+
+int pa_decode_workspace(const pa_decode_args* args, int64_t* bytes);
+int pa_decode_fwd(const pa_decode_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

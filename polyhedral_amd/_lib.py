@@ -14,7 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libpolyattn_amd.s
 PA_OK, PA_E_INVALID, PA_E_HIP, PA_E_UNSUPPORTED = 0, -1, -2, -3
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 MAX_TERMS = 8
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -45,6 +45,15 @@ class PaAttnArgs(ctypes.Structure):
                 ("wsel_sb", c_i64)]
 
 
+class PaDecodeArgs(ctypes.Structure):
+    _fields_ = [("q", c_vp), ("q_sb", c_i64), ("q_sn", c_i64), ("nq", c_i32), ("qpos0", c_i64),
+                ("k_cache", c_vp), ("v_cache", c_vp), ("c_sb", c_i64), ("c_sn", c_i64),
+                ("capacity", c_i64), ("length", c_i64), ("residue_s", c_i32), ("mask", PaMask),
+                ("BH", c_i64), ("D", c_i32), ("dtype", c_i32), ("scale", c_f32),
+                ("o", c_vp), ("o_sb", c_i64), ("o_sn", c_i64), ("lse", c_vp), ("lse_sb", c_i64),
+                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+
+
 # name -> (restype, argtypes); every symbol of include/polyattn_amd.h
 SIGNATURES = {
     "pa_last_error": (ctypes.c_char_p, []),
@@ -64,6 +73,10 @@ SIGNATURES = {
     "pa_attn_fwd": (ctypes.c_int, [ctypes.POINTER(PaAttnArgs), c_vp]),
     "pa_lse_merge": (ctypes.c_int, [ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), c_i32, c_vp, c_i32, c_vp,
                                     c_i64, c_i64, c_i32, c_vp]),
+    "pa_kv_append": (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32,
+                                    c_i64, c_i64, c_i32, c_vp]),
+    "pa_decode_workspace": (ctypes.c_int, [ctypes.POINTER(PaDecodeArgs), ctypes.POINTER(c_i64)]),
+    "pa_decode_fwd": (ctypes.c_int, [ctypes.POINTER(PaDecodeArgs), c_vp]),
 }
 
 _LIB = None

@@ -1,0 +1,507 @@
+// Decoding against a key / value cache kept in a class-A basis (gfx950).
+//
+// The reference relabels tokens for prefill only and leaves decoding open: new keys
+// arrive in original order and would have to be inserted at permuted positions
+// (docs/NOTES.md:2145-2153, 2201-2203).  With a cache of fixed capacity C, a multiple
+// of s, the residue-s basis gives every class its own segment of Q = C / s rows, and
+// the token at original position t sits at row (t mod s) Q + t div s: the end of its
+// class's segment.  Appending is one row write per token and tensor; cached rows never
+// move.  s = 1 is the identity basis.
+//
+// pa_kv_append writes the new rows.  pa_decode_fwd attends up to 8 query rows at
+// original positions qpos0 .. qpos0 + nq - 1 to the first `length` tokens under any
+// pa_mask, split over the keys: one work-group per (chunk of one class's segment, head)
+// writes a normalised partial and its log-sum-exp into the workspace, and a second
+// kernel merges the partials.  Keys are visited in 64-key blocks, one per wave and
+// one key per lane: a block with no live pair is not read at all, and in a block only
+// the live keys' K and V rows are read.  The bytes moved follow the live pairs in
+// either basis; what the relabelling saves is the visits to blocks with few live keys.
+#include <math.h>
+
+#include "common.hpp"
+
+namespace pa {
+namespace {
+
+constexpr int kDecMaxQ = 8;     // query rows per call
+constexpr int kDecWaves = 4;    // waves per work-group
+constexpr int kDecTarget = 2048;  // work-groups a split plan aims for
+
+typedef uint32_t du4 __attribute__((ext_vector_type(4)));
+
+struct DecK {
+  const char* q;
+  int64_t q_sb, q_sn;  // elements
+  const char* k;
+  const char* v;
+  int64_t c_sb, c_sn;  // elements
+  int64_t qpos0, length, Q, chunk;
+  int32_t nq, s, per_class, n_split;
+  float c;  // scale * log2(e)
+  Pred pred;
+  float* o_part;    // [BH][n_split][nq][D]
+  float* lse_part;  // [BH][n_split][nq]
+};
+
+// 16 bytes of a K row against 16 bytes of a query row, accumulated in fp32; one or two
+// output dimensions of a V row as floats.
+template <typename T>
+struct Dec;
+template <>
+struct Dec<__bf16> {
+  typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+  __device__ static float dot16(du4 k, du4 q, float acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t kw = k[e], qw = q[e];  // (scalar copies: bit-casting a vector element reads element 0)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(h2, kw), __builtin_bit_cast(h2, qw), acc, false);
+    }
+    return acc;
+  }
+  __device__ static float one(const char* p) { return (float)*reinterpret_cast<const __bf16*>(p); }
+  __device__ static void two(const char* p, float& x, float& y) {
+    const h2 v = *reinterpret_cast<const h2*>(p);
+    x = (float)v.x;
+    y = (float)v.y;
+  }
+};
+template <>
+struct Dec<_Float16> {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  __device__ static float dot16(du4 k, du4 q, float acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t kw = k[e], qw = q[e];
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, kw), __builtin_bit_cast(h2, qw), acc, false);
+    }
+    return acc;
+  }
+  __device__ static float one(const char* p) { return (float)*reinterpret_cast<const _Float16*>(p); }
+  __device__ static void two(const char* p, float& x, float& y) {
+    const h2 v = *reinterpret_cast<const h2*>(p);
+    x = (float)v.x;
+    y = (float)v.y;
+  }
+};
+template <>
+struct Dec<float> {
+  __device__ static float dot16(du4 k, du4 q, float acc) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t kw = k[e], qw = q[e];
+      acc = __builtin_fmaf(__builtin_bit_cast(float, kw), __builtin_bit_cast(float, qw), acc);
+    }
+    return acc;
+  }
+  __device__ static float one(const char* p) { return *reinterpret_cast<const float*>(p); }
+  __device__ static void two(const char* p, float& x, float& y) {
+    const float2 v = *reinterpret_cast<const float2*>(p);
+    x = v.x;
+    y = v.y;
+  }
+};
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// One work-group per (split, head).  Lane l of wave w scores key b0 + l of each block
+// b0 = i0 + 64 (w + 4 r); for P.V the lanes own output dimensions (D / 64 each) and
+// the block's live keys are taken 16 at a time.  MQ = 1 is the single-query case
+// (fewer registers), MQ = kDecMaxQ takes 2..8 queries.
+template <typename T, int D, int MQ>
+__global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
+  constexpr int ESZ = sizeof(T);
+  constexpr int RB = D * ESZ;     // row bytes
+  constexpr int NC = RB / 16;     // 16-byte chunks per row
+  constexpr int DPL = D / 64;     // output dimensions per lane
+  __shared__ __attribute__((aligned(16))) char q_lds[MQ * RB];
+  __shared__ float red_m[kDecWaves][MQ];
+  __shared__ float red_l[kDecWaves][MQ];
+  __shared__ float red_o[kDecWaves][MQ][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int split = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int nq = MQ == 1 ? 1 : a.nq;
+
+  for (int u = tid; u < nq * NC; u += 256) {
+    const int i = u / NC, cc = u - (u / NC) * NC;
+    *reinterpret_cast<du4*>(q_lds + i * RB + 16 * cc) =
+        *reinterpret_cast<const du4*>(a.q + (bh * a.q_sb + (int64_t)i * a.q_sn) * ESZ + 16 * cc);
+  }
+  __syncthreads();
+
+  // this split's keys: entries i0 .. i1 - 1 of class cls's segment
+  const int cls = split / a.per_class;
+  const int64_t jc = split - (int64_t)cls * a.per_class;
+  const int64_t cnt = a.length > cls ? (a.length - 1 - cls) / a.s + 1 : 0;
+  const int64_t i0 = jc * a.chunk;
+  const int64_t i1 = cnt < i0 + a.chunk ? cnt : i0 + a.chunk;
+  const char* kseg = a.k + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
+  const char* vseg = a.v + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
+  const int64_t rowb = a.c_sn * ESZ;
+
+  float m[MQ], lsum[MQ], o[MQ][DPL];
+#pragma unroll
+  for (int i = 0; i < MQ; ++i) {
+    m[i] = -1e30f;  // finite: exp2(m - m_new) is 0, never NaN
+    lsum[i] = 0.f;
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) o[i][d] = 0.f;
+  }
+
+  for (int64_t b0 = i0 + 64 * w; b0 < i1; b0 += 64 * kDecWaves) {
+    const int64_t idx = b0 + lane;
+    const int32_t t = (int32_t)(idx * a.s + cls);  // original position of this lane's key
+    uint32_t lv = 0u;                              // bit i: (query i, key) is live
+    if (idx < i1) {
+#pragma unroll
+      for (int i = 0; i < MQ; ++i)
+        if (i < nq && pred_live(a.pred, (int32_t)(a.qpos0 + i), t)) lv |= 1u << i;
+    }
+    const uint64_t any = __ballot(lv != 0u);
+    if (any == 0ull) continue;
+
+    du4 kr[NC];
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) kr[cc] = du4{0u, 0u, 0u, 0u};
+    if (lv) {
+      const char* kp = kseg + idx * rowb;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) kr[cc] = *reinterpret_cast<const du4*>(kp + 16 * cc);
+    }
+    float p[MQ];
+#pragma unroll
+    for (int i = 0; i < MQ; ++i) {
+      p[i] = 0.f;
+      if (i < nq) {
+        float acc = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc)
+          acc = Dec<T>::dot16(kr[cc], *reinterpret_cast<const du4*>(q_lds + i * RB + 16 * cc), acc);
+        const float x = ((lv >> i) & 1u) ? acc * a.c : -INFINITY;
+        const float mx = wave_max(x);
+        if (mx != -INFINITY) {
+          const float mn = fmaxf(m[i], mx);
+          const float alpha = exp2f(m[i] - mn);
+          m[i] = mn;
+          p[i] = exp2f(x - mn);
+          lsum[i] = lsum[i] * alpha + p[i];
+#pragma unroll
+          for (int d = 0; d < DPL; ++d) o[i][d] *= alpha;
+        }
+      }
+    }
+    // P.V over the live keys, 16 rows in flight at a time
+    uint64_t rem = any;
+    while (rem) {
+      int ks[16];
+      int nk = 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        ks[u] = 0;
+        if (rem) {
+          ks[u] = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(rem));
+          rem &= rem - 1;
+          nk = u + 1;
+        }
+      }
+      float vx[16][DPL];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (u < nk) {
+          const char* vp = vseg + (b0 + ks[u]) * rowb + lane * DPL * ESZ;
+          if constexpr (DPL == 2)
+            Dec<T>::two(vp, vx[u][0], vx[u][1]);
+          else
+            vx[u][0] = Dec<T>::one(vp);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (u < nk) {
+#pragma unroll
+          for (int i = 0; i < MQ; ++i) {
+            if (i < nq) {
+              const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), ks[u]));
+#pragma unroll
+              for (int d = 0; d < DPL; ++d) o[i][d] = __builtin_fmaf(pk, vx[u][d], o[i][d]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // the four waves' partials -> one normalised partial of the work-group
+#pragma unroll
+  for (int i = 0; i < MQ; ++i) {
+    if (i < nq) {
+      const float lt = wave_sum(lsum[i]);
+      if (lane == 0) {
+        red_m[w][i] = m[i];
+        red_l[w][i] = lt;
+      }
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) red_o[w][i][lane * DPL + d] = o[i][d];
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    for (int i = 0; i < nq; ++i) {
+      float M = red_m[0][i];
+#pragma unroll
+      for (int ww = 1; ww < kDecWaves; ++ww) M = fmaxf(M, red_m[ww][i]);
+      float L = 0.f, acc[DPL];
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kDecWaves; ++ww) {
+        const float f = exp2f(red_m[ww][i] - M);
+        L += f * red_l[ww][i];
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) acc[d] += f * red_o[ww][i][lane * DPL + d];
+      }
+      const int64_t row = (bh * a.n_split + split) * nq + i;
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) a.o_part[row * D + lane * DPL + d] = acc[d] * inv;
+      if (lane == 0) a.lse_part[row] = L > 0.f ? (M + log2f(L)) * 0.69314718055994530942f : -INFINITY;
+    }
+  }
+}
+
+// o[bh, i] = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M) over the splits; a row
+// whose every partial is empty gives 0 and lse -inf.
+template <typename T>
+__global__ __launch_bounds__(128) void decode_merge_kernel(const float* o_part, const float* lse_part, int n_split,
+                                                           int nq, int D, char* o, int64_t o_sb, int64_t o_sn,
+                                                           float* lse, int64_t lse_sb) {
+  const int64_t bh = blockIdx.x / nq;
+  const int i = blockIdx.x - (int)(bh * nq);
+  const int d = threadIdx.x;
+  const float* lp = lse_part + bh * n_split * nq + i;
+  float M = -INFINITY;
+  for (int sp = 0; sp < n_split; ++sp) M = fmaxf(M, lp[(int64_t)sp * nq]);
+  float den = 0.f, num = 0.f;
+  if (M != -INFINITY) {
+    for (int sp = 0; sp < n_split; ++sp) {
+      const float l = lp[(int64_t)sp * nq];
+      if (l == -INFINITY) continue;
+      const float f = expf(l - M);
+      den += f;
+      if (d < D) num += f * o_part[((bh * n_split + sp) * nq + i) * D + d];
+    }
+  }
+  if (d < D) {
+    const float v = den > 0.f ? num / den : 0.f;
+    *reinterpret_cast<T*>(o + ((bh * o_sb + (int64_t)i * o_sn) * (int64_t)sizeof(T)) + d * (int64_t)sizeof(T)) = (T)v;
+  }
+  if (lse && d == 0) lse[bh * lse_sb + i] = den > 0.f ? M + logf(den) : -INFINITY;
+}
+
+// Rows of the new tokens into their basis rows: unit u of row j of head bh of tensor
+// (K, V), 16- or 4-byte units.
+template <int VB>
+__global__ __launch_bounds__(256) void kv_append_kernel(const char* k_new, const char* v_new, int64_t n_sb,
+                                                        int64_t n_sn, char* kc, char* vc, int64_t c_sb,
+                                                        int64_t c_sn, int64_t BH, int64_t n, int32_t upr,
+                                                        int64_t pos0, int32_t s, int64_t Q) {
+  typedef uint32_t unit __attribute__((ext_vector_type(VB / 4)));
+  const int64_t total = 2 * BH * n * upr;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t u = g % upr;
+    int64_t r = g / upr;
+    const int64_t j = r % n;
+    r /= n;
+    const int64_t bh = r % BH;
+    const bool is_v = r >= BH;
+    const int64_t t = pos0 + j;
+    const int64_t row = (t % s) * Q + t / s;
+    const char* src = (is_v ? v_new : k_new) + bh * n_sb + j * n_sn + u * VB;
+    char* dst = (is_v ? vc : kc) + bh * c_sb + row * c_sn + u * VB;
+    *reinterpret_cast<unit*>(dst) = *reinterpret_cast<const unit*>(src);
+  }
+}
+
+struct Plan {
+  int32_t s, per_class, n_split;
+  int64_t chunk, Q;
+};
+
+// Split of the keys: every class's segment in chunks of a multiple of 256 keys (one
+// 64-key block per wave), enough chunks for about kDecTarget work-groups.
+Plan plan_of(int64_t BH, int64_t capacity, int64_t length, int32_t residue_s) {
+  Plan p;
+  p.s = residue_s > 1 ? residue_s : 1;
+  p.Q = capacity / p.s;
+  const int64_t cnt_max = (length + p.s - 1) / p.s;
+  int64_t per = (kDecTarget + BH * p.s - 1) / (BH * p.s);
+  if (per < 1) per = 1;
+  int64_t chunk = (cnt_max + per - 1) / per;
+  chunk = ((chunk + 255) / 256) * 256;
+  if (chunk < 256) chunk = 256;
+  p.chunk = chunk;
+  p.per_class = (int32_t)(cnt_max > 0 ? (cnt_max + chunk - 1) / chunk : 0);
+  p.n_split = p.s * p.per_class;
+  return p;
+}
+
+int check_decode(const pa_decode_args* x) {
+  PA_CHECK_ARG(x, "pa_decode: null arguments");
+  PA_CHECK_ARG(x->BH >= 1 && x->BH <= 65535, "pa_decode: BH=%lld not in 1..65535", (long long)x->BH);
+  PA_CHECK_ARG(x->nq >= 1 && x->nq <= kDecMaxQ, "pa_decode: nq=%d not in 1..%d", x->nq, kDecMaxQ);
+  PA_CHECK_ARG(x->dtype == PA_BF16 || x->dtype == PA_F16 || x->dtype == PA_F32, "pa_decode: dtype %d", x->dtype);
+  PA_CHECK_ARG(x->D == 128 || x->D == 64, "pa_decode: D=%d (64 or 128)", x->D);
+  PA_CHECK_ARG(x->dtype != PA_F32 || x->D == 64, "pa_decode: float32 needs D = 64");
+  const int32_t s = x->residue_s > 1 ? x->residue_s : 1;
+  PA_CHECK_ARG(x->capacity >= 1 && x->capacity < (1ll << 31) && x->capacity % s == 0,
+               "pa_decode: capacity=%lld must be in 1..2^31-1 and a multiple of s=%d", (long long)x->capacity, s);
+  PA_CHECK_ARG(x->length >= 0 && x->length <= x->capacity, "pa_decode: length=%lld outside 0..capacity",
+               (long long)x->length);
+  PA_CHECK_ARG(x->qpos0 >= 0 && x->qpos0 + x->nq <= (1ll << 31), "pa_decode: query positions out of range");
+  PA_CHECK_ARG(!x->mask.perm_q && !x->mask.perm_kv,
+               "pa_decode: the cache's basis is residue_s; the mask takes no permutation tables");
+  const int rc = check_mask(&x->mask, x->capacity > x->qpos0 + x->nq ? x->capacity : x->qpos0 + x->nq);
+  if (rc) return rc;
+  PA_CHECK_ARG(x->q && x->k_cache && x->v_cache && x->o, "pa_decode: null q / cache / o");
+  const int esz = x->dtype == PA_F32 ? 4 : 2;
+  auto al = [&](const void* ptr, int64_t sb, int64_t sn) {
+    return (reinterpret_cast<uintptr_t>(ptr) % 16) == 0 && (sb * esz) % 16 == 0 && (sn * esz) % 16 == 0;
+  };
+  PA_CHECK_ARG(al(x->q, x->q_sb, x->q_sn) && al(x->k_cache, x->c_sb, x->c_sn) && al(x->v_cache, x->c_sb, x->c_sn),
+               "pa_decode: q and cache rows must be 16-byte aligned");
+  PA_CHECK_ARG(x->c_sn >= x->D && x->q_sn >= x->D, "pa_decode: row strides below D");
+  return PA_OK;
+}
+
+template <typename T, int D>
+int launch_decode(const DecK& k, int64_t BH, hipStream_t s) {
+  if (k.nq == 1)
+    hipLaunchKernelGGL((decode_kernel<T, D, 1>), dim3((unsigned)k.n_split, (unsigned)BH), dim3(256), 0, s, k);
+  else
+    hipLaunchKernelGGL((decode_kernel<T, D, kDecMaxQ>), dim3((unsigned)k.n_split, (unsigned)BH), dim3(256), 0, s,
+                       k);
+  PA_LAUNCH_CHECK("decode_kernel");
+  return PA_OK;
+}
+
+}  // namespace
+}  // namespace pa
+
+extern "C" int pa_decode_workspace(const pa_decode_args* x, int64_t* bytes) {
+  const int rc = pa::check_decode(x);
+  if (rc) return rc;
+  PA_CHECK_ARG(bytes, "pa_decode_workspace: null output");
+  const pa::Plan p = pa::plan_of(x->BH, x->capacity, x->length, x->residue_s);
+  *bytes = x->BH * (int64_t)p.n_split * x->nq * (x->D + 1) * 4;
+  return PA_OK;
+}
+
+extern "C" int pa_decode_fwd(const pa_decode_args* x, void* stream) {
+  const int rc = pa::check_decode(x);
+  if (rc) return rc;
+  const pa::Plan p = pa::plan_of(x->BH, x->capacity, x->length, x->residue_s);
+  const int64_t need = x->BH * (int64_t)p.n_split * x->nq * (x->D + 1) * 4;
+  PA_CHECK_ARG(p.n_split == 0 || (x->workspace && x->workspace_bytes >= need &&
+                                  (reinterpret_cast<uintptr_t>(x->workspace) % 16) == 0),
+               "pa_decode_fwd: workspace of %lld bytes (16-byte aligned) needed, got %lld", (long long)need,
+               (long long)x->workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  pa::DecK k;
+  k.q = static_cast<const char*>(x->q);
+  k.q_sb = x->q_sb;
+  k.q_sn = x->q_sn;
+  k.k = static_cast<const char*>(x->k_cache);
+  k.v = static_cast<const char*>(x->v_cache);
+  k.c_sb = x->c_sb;
+  k.c_sn = x->c_sn;
+  k.qpos0 = x->qpos0;
+  k.length = x->length;
+  k.Q = p.Q;
+  k.chunk = p.chunk;
+  k.nq = x->nq;
+  k.s = p.s;
+  k.per_class = p.per_class;
+  k.n_split = p.n_split;
+  k.c = (x->scale > 0.f ? x->scale : 1.f / sqrtf((float)x->D)) * 1.4426950408889634f;
+  k.pred = pa::make_pred(x->mask);
+  float* ws = static_cast<float*>(x->workspace);
+  k.o_part = ws;
+  k.lse_part = ws ? ws + x->BH * (int64_t)p.n_split * x->nq * x->D : nullptr;
+  if (p.n_split > 0) {
+    int r = PA_OK;
+    if (x->dtype == PA_BF16)
+      r = x->D == 128 ? pa::launch_decode<__bf16, 128>(k, x->BH, s) : pa::launch_decode<__bf16, 64>(k, x->BH, s);
+    else if (x->dtype == PA_F16)
+      r = x->D == 128 ? pa::launch_decode<_Float16, 128>(k, x->BH, s) : pa::launch_decode<_Float16, 64>(k, x->BH, s);
+    else
+      r = pa::launch_decode<float, 64>(k, x->BH, s);
+    if (r) return r;
+  }
+  const unsigned g = (unsigned)(x->BH * x->nq);
+  char* o = static_cast<char*>(x->o);
+#define PA_MERGE(TT)                                                                                            \
+  hipLaunchKernelGGL((pa::decode_merge_kernel<TT>), dim3(g), dim3(128), 0, s, k.o_part, k.lse_part, p.n_split,  \
+                     x->nq, x->D, o, x->o_sb, x->o_sn, x->lse, x->lse_sb)
+  if (x->dtype == PA_BF16)
+    PA_MERGE(__bf16);
+  else if (x->dtype == PA_F16)
+    PA_MERGE(_Float16);
+  else
+    PA_MERGE(float);
+#undef PA_MERGE
+  PA_LAUNCH_CHECK("decode_merge_kernel");
+  return PA_OK;
+}
+
+extern "C" int pa_kv_append(const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sn, void* k_cache,
+                            void* v_cache, int64_t c_sb, int64_t c_sn, int64_t BH, int64_t n, int32_t D,
+                            int32_t dtype, int64_t capacity, int64_t pos0, int32_t residue_s, void* stream) {
+  PA_CHECK_ARG(dtype == PA_BF16 || dtype == PA_F16 || dtype == PA_F32, "pa_kv_append: dtype %d", dtype);
+  const int64_t s = residue_s > 1 ? residue_s : 1;
+  PA_CHECK_ARG(BH >= 1 && n >= 0 && D >= 1, "pa_kv_append: BH=%lld n=%lld D=%d", (long long)BH, (long long)n, D);
+  PA_CHECK_ARG(capacity >= 1 && capacity % s == 0, "pa_kv_append: capacity=%lld not a multiple of s=%lld",
+               (long long)capacity, (long long)s);
+  PA_CHECK_ARG(pos0 >= 0 && pos0 + n <= capacity, "pa_kv_append: positions %lld..%lld exceed capacity %lld",
+               (long long)pos0, (long long)(pos0 + n), (long long)capacity);
+  if (n == 0) return PA_OK;
+  PA_CHECK_ARG(k_new && v_new && k_cache && v_cache, "pa_kv_append: null pointer");
+  const int esz = dtype == PA_F32 ? 4 : 2;
+  const int64_t rb = (int64_t)D * esz;
+  PA_CHECK_ARG(rb % 4 == 0, "pa_kv_append: row bytes %lld not a multiple of 4", (long long)rb);
+  PA_CHECK_ARG(c_sn >= D && new_sn >= D, "pa_kv_append: row strides below D");
+  auto al = [](const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; };
+  const bool v16 = rb % 16 == 0 && al(k_new, 16) && al(v_new, 16) && al(k_cache, 16) && al(v_cache, 16) &&
+                   (new_sb * esz) % 16 == 0 && (new_sn * esz) % 16 == 0 && (c_sb * esz) % 16 == 0 &&
+                   (c_sn * esz) % 16 == 0;
+  PA_CHECK_ARG(v16 || (al(k_new, 4) && al(v_new, 4) && al(k_cache, 4) && al(v_cache, 4)),
+               "pa_kv_append: pointers must be 4-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int VB = v16 ? 16 : 4;
+  const int32_t upr = (int32_t)(rb / VB);
+  int64_t blocks = (2 * BH * n * upr + 255) / 256;
+  if (blocks > (1 << 20)) blocks = 1 << 20;
+  const char* kn = static_cast<const char*>(k_new);
+  const char* vn = static_cast<const char*>(v_new);
+  char* kc = static_cast<char*>(k_cache);
+  char* vc = static_cast<char*>(v_cache);
+  if (v16)
+    hipLaunchKernelGGL(pa::kv_append_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, st, kn, vn, new_sb * esz,
+                       new_sn * esz, kc, vc, c_sb * esz, c_sn * esz, BH, n, upr, pos0, (int32_t)s, capacity / s);
+  else
+    hipLaunchKernelGGL(pa::kv_append_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, st, kn, vn, new_sb * esz,
+                       new_sn * esz, kc, vc, c_sb * esz, c_sn * esz, BH, n, upr, pos0, (int32_t)s, capacity / s);
+  PA_LAUNCH_CHECK("kv_append_kernel");
+  return PA_OK;
+}

@@ -1,0 +1,143 @@
+"""Decoding against a cache kept in a class-A basis (pa_kv_append, pa_decode_fwd).
+
+The cache layout is pinned by the residue permutation's closed form (oracle.permute,
+gpu/permute.py:12-15): row r of a capacity-C cache in the residue-s basis holds the
+token at original position residue_perm(C, s)[r].  Decode attention is pinned by the
+float64 oracle (gpu/reference.py:5-17) on the same tokens in original order: the
+query rows at positions qpos0 .. qpos0 + nq - 1 against the first `length` keys."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import masks as om
+from oracle import permute as op
+from polyhedral_amd import _lib
+from polyhedral_amd import decode as pdec
+from polyhedral_amd.polyattn import masks as pm
+from polyhedral_amd.registry import numpy_mask
+from tests.util import as64, check_close, make_qkv
+
+pytestmark = pytest.mark.gpu
+
+
+def _orig_of_row(capacity, s):
+    return op.residue_perm(capacity, s) if s > 1 else np.arange(capacity)
+
+
+def _fill(cache, k, v, sizes, gpu):
+    t0 = 0
+    for n in sizes:
+        cache.append(k[:, t0:t0 + n].to(gpu), v[:, t0:t0 + n].to(gpu))
+        t0 += n
+    assert cache.length == t0
+    return t0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("residue", [0, 8, 16])
+def test_append_places_rows_by_the_residue_permutation(gpu, residue, dtype):
+    BH, cap = 3, 2048
+    D = 64 if dtype == torch.float32 else 128
+    _, k, v = make_qkv(BH, cap, D, dtype, seed=residue + 1)
+    cache = pdec.KVCache(BH, cap, D, dtype, residue, gpu)
+    L = _fill(cache, k, v, [700, 1, 1, 5, 300, 1], gpu)
+    orig = _orig_of_row(cap, max(residue, 1))
+    assert np.array_equal(cache.rows(orig), np.arange(cap))   # rows() inverts the permutation
+    filled = np.flatnonzero(orig < L)
+    empty = np.flatnonzero(orig >= L)
+    for got, want in ((cache.k.cpu(), k), (cache.v.cpu(), v)):
+        assert torch.equal(got[:, filled], want[:, orig[filled]])
+        assert torch.count_nonzero(got[:, empty]) == 0
+
+
+@pytest.mark.parametrize("nq", [1, 3, 8])
+@pytest.mark.parametrize("residue", [0, 8, 16])
+@pytest.mark.parametrize("name", ["dilated-8", "band256+lat16", "sinks4+win256", "causal", "window-128",
+                                  "lat16-band256", "local256+str8", "prefixlm-2048"])
+def test_decode_equals_oracle(gpu, name, residue, nq):
+    BH, cap, D, L = 2, 2048, 128, 1500
+    q, k, v = make_qkv(BH, cap, D, torch.bfloat16, seed=nq)
+    cache = pdec.KVCache(BH, cap, D, torch.bfloat16, residue, gpu)
+    _fill(cache, k, v, [L - 8, 3, 5], gpu)
+    qpos0 = L - nq
+    lse = torch.empty(BH, nq, device=gpu)
+    out = cache.attend(q[:, qpos0:L].to(gpu), numpy_mask(name), lse=lse)
+    spec = om.NAMED[name]
+    want, want_lse = oatt.dense_attention(as64(q[:, qpos0:L]), as64(k[:, :L]), as64(v[:, :L]),
+                                          lambda r0, r1: om.rows(spec, qpos0 + r0, qpos0 + r1, L))
+    check_close(out, want, torch.bfloat16, f"decode {name} s={residue} nq={nq}")
+    fin = np.isfinite(want_lse)
+    got_lse = lse.cpu().numpy()
+    assert np.array_equal(np.isfinite(got_lse), fin)
+    assert np.abs(got_lse[fin] - want_lse[fin]).max() < 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_decode_other_dtypes_and_earlier_queries(gpu, dtype):
+    """Queries anywhere before the end, and a prefix of the cache (length < tokens held)."""
+    BH, cap, name = 2, 1024, "band256+lat16"
+    D = 64 if dtype == torch.float32 else 128
+    q, k, v = make_qkv(BH, cap, D, dtype, seed=4)
+    cache = pdec.KVCache(BH, cap, D, dtype, 16, gpu)
+    _fill(cache, k, v, [900], gpu)
+    for qpos0, nq, L in ((100, 4, 900), (500, 1, 700), (0, 2, 900)):
+        out = cache.attend(q[:, qpos0:qpos0 + nq].to(gpu), numpy_mask(name), qpos0=qpos0, length=L)
+        want, _ = oatt.dense_attention(as64(q[:, qpos0:qpos0 + nq]), as64(k[:, :L]), as64(v[:, :L]),
+                                       lambda r0, r1: om.rows(om.NAMED[name], qpos0 + r0, qpos0 + r1, L))
+        check_close(out, want, dtype, f"decode {dtype} qpos0={qpos0} nq={nq} L={L}")
+
+
+def test_dead_queries_and_empty_cache(gpu):
+    BH, cap, D = 2, 512, 128
+    q, k, v = make_qkv(BH, cap, D, torch.bfloat16, seed=2)
+    M = om.dense(om.NAMED["causal"], cap)
+    M[300] = False                      # query 300 sees no key
+    cache = pdec.KVCache(BH, cap, D, torch.bfloat16, 8, gpu)
+    lse = torch.empty(BH, 1, device=gpu)
+    out = cache.attend(q[:, :1].to(gpu), pm.DenseMask(M), qpos0=0, lse=lse)   # empty cache
+    assert torch.count_nonzero(out) == 0 and torch.isinf(lse).all() and (lse < 0).all()
+    _fill(cache, k, v, [301], gpu)
+    lse = torch.empty(BH, 2, device=gpu)
+    out = cache.attend(q[:, 299:301].to(gpu), pm.DenseMask(M), lse=lse)
+    assert torch.count_nonzero(out[:, 1]) == 0 and torch.isinf(lse[:, 1]).all()
+    want, _ = oatt.dense_attention(as64(q[:, 299:300]), as64(k[:, :301]), as64(v[:, :301]),
+                                   lambda r0, r1: M[299 + r0:299 + r1, :301])
+    check_close(out[:, :1], want, torch.bfloat16, "dense mask decode")
+
+
+def test_bases_agree_at_the_headline_size(gpu):
+    """band-256 | lattice-16, L = 16384, 32 heads, D = 128: the newest token decoded in the
+    identity and the rp16 basis; both against the oracle on two heads."""
+    H, L, D, name = 32, 16384, 128, "band256+lat16"
+    q, k, v = make_qkv(H, L, D, torch.bfloat16, seed=0)
+    outs = []
+    for s in (0, 16):
+        cache = pdec.KVCache(H, L, D, torch.bfloat16, s, gpu)
+        _fill(cache, k, v, [L - 1, 1], gpu)
+        outs.append(cache.attend(q[:, L - 1:].to(gpu), numpy_mask(name)).float().cpu())
+        del cache
+    want, _ = oatt.dense_attention(as64(q[:2, L - 1:]), as64(k[:2]), as64(v[:2]),
+                                   lambda r0, r1: om.rows(om.NAMED[name], L - 1 + r0, L - 1 + r1, L))
+    for o in outs:
+        check_close(o[:2], want, torch.bfloat16, "headline decode")
+    assert (outs[0] - outs[1]).abs().max().item() < 2e-2
+
+
+def test_decode_argument_errors(gpu):
+    BH, cap, D = 1, 256, 128
+    cache = pdec.KVCache(BH, cap, D, torch.bfloat16, 16, gpu)
+    q = torch.zeros(BH, 9, D, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="1..8"):
+        cache.attend(q, numpy_mask("causal"), qpos0=0)
+    with pytest.raises(ValueError, match="capacity"):
+        cache.append(torch.zeros(BH, 257, D, dtype=torch.bfloat16, device=gpu),
+                     torch.zeros(BH, 257, D, dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(ValueError, match="multiple"):
+        pdec.KVCache(BH, 250, D, torch.bfloat16, 16, gpu)
+    # the C ABI checks the same bounds itself
+    z = torch.zeros(BH, 2, D, dtype=torch.bfloat16, device=gpu)
+    rc = _lib.lib().pa_kv_append(_lib.ptr(z), _lib.ptr(z), z.stride(0), z.stride(1), _lib.ptr(cache.k),
+                                 _lib.ptr(cache.v), cache.k.stride(0), cache.k.stride(1), BH, 2, D, _lib.PA_BF16,
+                                 cap, cap - 1, 16, _lib.stream_of(z))
+    assert rc == _lib.PA_E_INVALID and b"capacity" in _lib.lib().pa_last_error()
