@@ -131,6 +131,76 @@ def measure_permute(q, k, v, s, reps=50, warmup=10):
                      "pa_permute_stack launch (Q, K, V and the position ids), scatter_o one pa_permute_rows")
 
 
+def measure_decode(wl, q, k, v, residues=(0, 16), reps=200, warmup=20):
+    """One decode step of the workload's mask against a cache of all L tokens: the newest
+    token's K / V appended (pa_kv_append, rewriting the same row every step) and its query
+    row attended to the cache (pa_decode_fwd, split kernel + merge), captured in a HIP
+    graph and replayed (the step is a few microseconds of kernels; eager launches would
+    time the host).  Algorithmic bytes: the live keys' K and V rows, the appended rows,
+    q and o."""
+    import ctypes
+
+    import torch
+
+    from polyhedral_amd import _lib
+    from polyhedral_amd import decode as pdec
+    H, L, D = wl.H, wl.L, wl.D
+    live = int(np.asarray(wl.union.row_cols(L - 1, L), dtype=bool).sum())
+    rb = D * q.element_size()
+    nbytes = H * (2 * live * rb + 2 * rb + 2 * rb)
+    out = {}
+    for s in residues:
+        cache = pdec.KVCache(H, L, D, q.dtype, s, q.device)
+        cache.append(k[:, :L - 1], v[:, :L - 1])
+        kn, vn = k[:, L - 1:].contiguous(), v[:, L - 1:].contiguous()
+        cache.append(kn, vn)
+        launch = cache.prepare(q[:, L - 1:].contiguous(), wl.union)
+        lib = _lib.lib()
+        app_args = (_lib.ptr(kn), _lib.ptr(vn), kn.stride(0), kn.stride(1), _lib.ptr(cache.k), _lib.ptr(cache.v),
+                    cache.k.stride(0), cache.k.stride(1), H, 1, D, _lib.dtype_code(kn), L, L - 1, cache.residue)
+
+        def step():
+            _lib.check(lib.pa_kv_append(*app_args, _lib.stream_of(kn)), "pa_kv_append")
+            launch()
+
+        step()
+        torch.cuda.synchronize()
+        eager_out = launch.out.clone()
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        same = torch.equal(launch.out, eager_out)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(reps):
+            g.replay()
+        ev[1].record()
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / reps
+        # eager steps for comparison (host launch overhead included)
+        t0 = time.perf_counter()
+        for _ in range(50):
+            step()
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / 50
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out["identity" if s <= 1 else f"rp{s}"] = dict(
+            ms_per_token=round(ms, 5), eager_ms_per_token=round(eager_ms, 5), tokens_per_s=round(1e3 / ms, 1),
+            graph_equals_eager=same, bytes=nbytes, gb_per_s=round(gbs, 1),
+            roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_GBPS, unit="GB/s",
+                          frac=round(gbs / HBM_GBPS, 5)))
+        del cache, launch, g
+    return dict(live_keys=live, heads=H, context=L, note="one decode step (append + attend), batch 1, "
+                "HIP graph replay; algorithmic bytes = live K/V rows + appended rows + q + o", **out)
+
+
 def cpu_baseline(wl, budget_s=12.0):
     """Oracle dense fp32 attention on the host over (head, 1024-row chunk) units in
     order until the budget is spent; live-FLOP TFLOP/s over what was processed."""
@@ -217,6 +287,8 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     iso_ms = measure_isolated(launches, max(25, min(steps, 100)))
     residues = [b["piece"].residue for b in plan.built if b["piece"].residue]
     permute = measure_permute(q, k, v, residues[0]) if residues and variant is None else None
+    decode = (measure_decode(wl, q, k, v, (0,) + tuple(sorted(set(residues))))
+              if variant is None and wl.D in (64, 128) and wl.dtype != torch.float32 else None)
     kernels = ["attn_stream_kernel" if x.kernel == "stream" else "attn_fwd_kernel" for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
     for i, bi in enumerate(plan.launched):
@@ -250,6 +322,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
                                     "between forwards, median (gpu/bench.py:11-24 with a flush larger than the "
                                     "memory-side cache)")
     res["permute"] = permute
+    res["decode"] = decode
     res["_launches"] = len(launches)
     if with_cpu:
         log(f"[bench] cpu baseline for {name} ...")
@@ -310,6 +383,11 @@ def main():
                     ib = r["index_build"]
                     log(f"[bench]   index build: device {ib['gpu_ms']:.2f} ms, host C builder {ib['cpu_ms']:.1f} ms "
                         f"on {ib['cpu_threads']} threads ({ib['speedup']:.0f}x)")
+                if r.get("decode"):
+                    dd = r["decode"]
+                    log("[bench]   decode (append + attend, 1 token): " + ", ".join(
+                        f"{b} {dd[b]['ms_per_token'] * 1e3:.1f} us ({dd[b]['gb_per_s']:.0f} GB/s)"
+                        for b in dd if isinstance(dd[b], dict)))
                 if r.get("permute"):
                     pm_ = r["permute"]
                     log(f"[bench]   permute rp{pm_['residue']}: Q/K/V gather {pm_['gather_qkv']['gb_per_s']:.0f} GB/s, "
@@ -341,6 +419,7 @@ def main():
         index_build=r.get("index_build"),
         isolated=r["isolated"],
         permute=r["permute"],
+        decode=r["decode"],
     )
     print(json.dumps(line), flush=True)
 

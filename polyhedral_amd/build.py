@@ -46,7 +46,7 @@ def _torch_lib():
 
 # per-source additions: the streaming kernel computes no NaN on purpose (masked scores
 # are -inf, never NaN), so fmax needs no NaN-quieting instructions
-EXTRA_FLAGS = {"attn_stream.hip": ["-fno-honor-nans", "-Wno-inline-asm"]}
+EXTRA_FLAGS = {"attn_stream.hip": ["-fno-honor-nans", "-Wno-inline-asm"], "decode.hip": ["-Wno-inline-asm"]}
 
 
 def _compile(src, hipcc):

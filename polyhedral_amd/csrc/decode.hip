@@ -25,7 +25,8 @@ namespace {
 
 constexpr int kDecMaxQ = 8;     // query rows per call
 constexpr int kDecWaves = 4;    // waves per work-group
-constexpr int kDecTarget = 2048;  // work-groups a split plan aims for
+constexpr int kDecTarget = 768;    // work-groups a split plan aims for
+constexpr int kMergeMax = 4096;    // splits per (head, query) the merge takes
 
 typedef uint32_t du4 __attribute__((ext_vector_type(4)));
 
@@ -58,12 +59,9 @@ struct Dec<__bf16> {
     }
     return acc;
   }
-  __device__ static float one(const char* p) { return (float)*reinterpret_cast<const __bf16*>(p); }
-  __device__ static void two(const char* p, float& x, float& y) {
-    const h2 v = *reinterpret_cast<const h2*>(p);
-    x = (float)v.x;
-    y = (float)v.y;
-  }
+  // the lane's V word: one (low 16 bits) or two elements
+  __device__ static float lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+  __device__ static float hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 };
 template <>
 struct Dec<_Float16> {
@@ -76,12 +74,8 @@ struct Dec<_Float16> {
     }
     return acc;
   }
-  __device__ static float one(const char* p) { return (float)*reinterpret_cast<const _Float16*>(p); }
-  __device__ static void two(const char* p, float& x, float& y) {
-    const h2 v = *reinterpret_cast<const h2*>(p);
-    x = (float)v.x;
-    y = (float)v.y;
-  }
+  __device__ static float lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu)); }
+  __device__ static float hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
 };
 template <>
 struct Dec<float> {
@@ -93,13 +87,14 @@ struct Dec<float> {
     }
     return acc;
   }
-  __device__ static float one(const char* p) { return *reinterpret_cast<const float*>(p); }
-  __device__ static void two(const char* p, float& x, float& y) {
-    const float2 v = *reinterpret_cast<const float2*>(p);
-    x = v.x;
-    y = v.y;
-  }
+  __device__ static float lo(uint32_t w) { return __builtin_bit_cast(float, w); }
+  __device__ static float hi(uint32_t w) { return __builtin_bit_cast(float, w); }
 };
+
+// LDS DMA of 16 bytes per lane: lane l writes LDS[m0 + 16 l] from gbase + voff.
+__device__ __forceinline__ void lds_dma16(uint32_t m0, const char* gbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+}
 
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
@@ -113,23 +108,29 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // One work-group per (split, head).  Lane l of wave w scores key b0 + l of each block
-// b0 = i0 + 64 (w + 4 r); for P.V the lanes own output dimensions (D / 64 each) and
-// the block's live keys are taken 16 at a time.  MQ = 1 is the single-query case
-// (fewer registers), MQ = kDecMaxQ takes 2..8 queries.
+// b0 = i0 + 64 (w + 4 r) from its K row; the V rows of the block's live keys go by LDS
+// DMA into the wave's 64-row buffer, and for P.V the lanes own output dimensions
+// (D / 64 each).  MQ = 1 is the single-query case (fewer registers), MQ = kDecMaxQ
+// takes 2..8 queries.
 template <typename T, int D, int MQ>
 __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
   constexpr int ESZ = sizeof(T);
   constexpr int RB = D * ESZ;     // row bytes
   constexpr int NC = RB / 16;     // 16-byte chunks per row
   constexpr int DPL = D / 64;     // output dimensions per lane
+  constexpr int LPR = RB / 16;    // DMA lanes per row
+  constexpr int RPI = 64 / LPR;   // rows per DMA instruction
+  // the waves' V buffers; after the key loop the same LDS holds the cross-wave partials
+  __shared__ __attribute__((aligned(16))) char vbuf[kDecWaves * 64 * RB];
   __shared__ __attribute__((aligned(16))) char q_lds[MQ * RB];
   __shared__ float red_m[kDecWaves][MQ];
   __shared__ float red_l[kDecWaves][MQ];
-  __shared__ float red_o[kDecWaves][MQ][D];
+  static_assert(sizeof(float) * kDecWaves * MQ * D <= sizeof(vbuf), "partials fit the V buffers");
+  float(*red_o)[MQ][D] = reinterpret_cast<float(*)[MQ][D]>(vbuf);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int split = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const int nq = MQ == 1 ? 1 : a.nq;
@@ -172,6 +173,19 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
     const uint64_t any = __ballot(lv != 0u);
     if (any == 0ull) continue;
 
+    // the V rows of the keys live for some query, into this wave's buffer (lanes of a dead
+    // row are masked off; a DMA instruction whose rows are all dead is skipped), and the
+    // K row of each live key, one per lane, all in flight together
+    const char* vblk = vseg + b0 * rowb;
+    const uint32_t vbw = (uint32_t)(uintptr_t)(vbuf + w * 64 * RB);
+#pragma unroll
+    for (int r = 0; r < 64 / RPI; ++r) {
+      if ((any >> (r * RPI)) & ((1ull << RPI) - 1ull)) {
+        const int row = r * RPI + lane / LPR;
+        if ((any >> row) & 1ull)
+          lds_dma16(vbw + r * 1024, vblk, (uint32_t)(row * rowb + 16 * (lane % LPR)));
+      }
+    }
     du4 kr[NC];
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) kr[cc] = du4{0u, 0u, 0u, 0u};
@@ -202,46 +216,33 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
         }
       }
     }
-    // P.V over the live keys, 16 rows in flight at a time
-    uint64_t rem = any;
-    while (rem) {
-      int ks[16];
-      int nk = 0;
+    // P.V over the live keys, V from the buffer (this wave's own DMA: waiting for it is enough)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const char* vrow = vbuf + w * 64 * RB + lane * DPL * ESZ;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        ks[u] = 0;
-        if (rem) {
-          ks[u] = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(rem));
-          rem &= rem - 1;
-          nk = u + 1;
-        }
-      }
-      float vx[16][DPL];
+    for (int u = 0; u < 64; ++u) {
+      if ((any >> u) & 1ull) {
+        uint32_t vw;
+        if constexpr (DPL * ESZ == 4)
+          vw = *reinterpret_cast<const uint32_t*>(vrow + u * RB);
+        else
+          vw = *reinterpret_cast<const uint16_t*>(vrow + u * RB);
+        float vx[DPL];
+        vx[0] = Dec<T>::lo(vw);
+        if constexpr (DPL == 2) vx[DPL - 1] = Dec<T>::hi(vw);
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        if (u < nk) {
-          const char* vp = vseg + (b0 + ks[u]) * rowb + lane * DPL * ESZ;
-          if constexpr (DPL == 2)
-            Dec<T>::two(vp, vx[u][0], vx[u][1]);
-          else
-            vx[u][0] = Dec<T>::one(vp);
-        }
-      }
+        for (int i = 0; i < MQ; ++i) {
+          if (i < nq) {
+            const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), u));
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        if (u < nk) {
-#pragma unroll
-          for (int i = 0; i < MQ; ++i) {
-            if (i < nq) {
-              const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), ks[u]));
-#pragma unroll
-              for (int d = 0; d < DPL; ++d) o[i][d] = __builtin_fmaf(pk, vx[u][d], o[i][d]);
-            }
+            for (int d = 0; d < DPL; ++d) o[i][d] = __builtin_fmaf(pk, vx[d], o[i][d]);
           }
         }
       }
     }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // buffer reads done before the next DMA
   }
+  __syncthreads();  // every wave is past its buffer: it now holds the partials
 
   // the four waves' partials -> one normalised partial of the work-group
 #pragma unroll
@@ -282,32 +283,64 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
 }
 
 // o[bh, i] = sum_s exp(lse_s - M) o_s / sum_s exp(lse_s - M) over the splits; a row
-// whose every partial is empty gives 0 and lse -inf.
+// whose every partial is empty gives 0 and lse -inf.  One work-group per (bh, i): the
+// weights are computed once into LDS, then 256 / D groups of D threads share the splits.
 template <typename T>
-__global__ __launch_bounds__(128) void decode_merge_kernel(const float* o_part, const float* lse_part, int n_split,
+__global__ __launch_bounds__(256) void decode_merge_kernel(const float* o_part, const float* lse_part, int n_split,
                                                            int nq, int D, char* o, int64_t o_sb, int64_t o_sn,
                                                            float* lse, int64_t lse_sb) {
+  __shared__ float wts[kMergeMax];
+  __shared__ float red[256];
   const int64_t bh = blockIdx.x / nq;
   const int i = blockIdx.x - (int)(bh * nq);
-  const int d = threadIdx.x;
+  const int tid = threadIdx.x;
   const float* lp = lse_part + bh * n_split * nq + i;
   float M = -INFINITY;
-  for (int sp = 0; sp < n_split; ++sp) M = fmaxf(M, lp[(int64_t)sp * nq]);
-  float den = 0.f, num = 0.f;
-  if (M != -INFINITY) {
-    for (int sp = 0; sp < n_split; ++sp) {
-      const float l = lp[(int64_t)sp * nq];
-      if (l == -INFINITY) continue;
-      const float f = expf(l - M);
-      den += f;
-      if (d < D) num += f * o_part[((bh * n_split + sp) * nq + i) * D + d];
-    }
+  for (int sp = tid; sp < n_split; sp += 256) {
+    const float l = lp[(int64_t)sp * nq];
+    wts[sp] = l;
+    M = fmaxf(M, l);
   }
-  if (d < D) {
+  red[tid] = M;
+  __syncthreads();
+  for (int h = 128; h >= 1; h >>= 1) {
+    if (tid < h) red[tid] = fmaxf(red[tid], red[tid + h]);
+    __syncthreads();
+  }
+  M = red[0];
+  __syncthreads();
+  float den = 0.f;
+  for (int sp = tid; sp < n_split; sp += 256) {
+    const float l = wts[sp];
+    const float f = (M == -INFINITY || l == -INFINITY) ? 0.f : expf(l - M);
+    wts[sp] = f;
+    den += f;
+  }
+  red[tid] = den;
+  __syncthreads();
+  for (int h = 128; h >= 1; h >>= 1) {
+    if (tid < h) red[tid] += red[tid + h];
+    __syncthreads();
+  }
+  den = red[0];
+  __syncthreads();
+  const int parts = 256 / D;
+  const int d = tid % D, part = tid / D;
+  float num = 0.f;
+  if (part < parts) {
+    // (an empty split's partial is 0 and its weight 0: no branch in the loop)
+    const float* op = o_part + (bh * n_split * nq + i) * D + d;
+#pragma unroll 8
+    for (int sp = part; sp < n_split; sp += parts) num = __builtin_fmaf(wts[sp], op[(int64_t)sp * nq * D], num);
+  }
+  red[tid] = num;
+  __syncthreads();
+  if (tid < D) {
+    for (int pp = 1; pp < parts; ++pp) num += red[pp * D + tid];
     const float v = den > 0.f ? num / den : 0.f;
-    *reinterpret_cast<T*>(o + ((bh * o_sb + (int64_t)i * o_sn) * (int64_t)sizeof(T)) + d * (int64_t)sizeof(T)) = (T)v;
+    *reinterpret_cast<T*>(o + ((bh * o_sb + (int64_t)i * o_sn) * (int64_t)sizeof(T)) + tid * (int64_t)sizeof(T)) = (T)v;
   }
-  if (lse && d == 0) lse[bh * lse_sb + i] = den > 0.f ? M + logf(den) : -INFINITY;
+  if (lse && tid == 0) lse[bh * lse_sb + i] = den > 0.f ? M + logf(den) : -INFINITY;
 }
 
 // Rows of the new tokens into their basis rows: unit u of row j of head bh of tensor
@@ -351,6 +384,8 @@ Plan plan_of(int64_t BH, int64_t capacity, int64_t length, int32_t residue_s) {
   int64_t chunk = (cnt_max + per - 1) / per;
   chunk = ((chunk + 255) / 256) * 256;
   if (chunk < 256) chunk = 256;
+  // the merge holds one weight per split in LDS
+  while (p.s * ((cnt_max + chunk - 1) / chunk) > kMergeMax) chunk *= 2;
   p.chunk = chunk;
   p.per_class = (int32_t)(cnt_max > 0 ? (cnt_max + chunk - 1) / chunk : 0);
   p.n_split = p.s * p.per_class;
@@ -452,7 +487,7 @@ extern "C" int pa_decode_fwd(const pa_decode_args* x, void* stream) {
   const unsigned g = (unsigned)(x->BH * x->nq);
   char* o = static_cast<char*>(x->o);
 #define PA_MERGE(TT)                                                                                            \
-  hipLaunchKernelGGL((pa::decode_merge_kernel<TT>), dim3(g), dim3(128), 0, s, k.o_part, k.lse_part, p.n_split,  \
+  hipLaunchKernelGGL((pa::decode_merge_kernel<TT>), dim3(g), dim3(256), 0, s, k.o_part, k.lse_part, p.n_split,  \
                      x->nq, x->D, o, x->o_sb, x->o_sn, x->lse, x->lse_sb)
   if (x->dtype == PA_BF16)
     PA_MERGE(__bf16);
