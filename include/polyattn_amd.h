@@ -277,6 +277,52 @@ typedef struct pa_decode_args {
 int pa_decode_workspace(const pa_decode_args* args, int64_t* bytes);
 int pa_decode_fwd(const pa_decode_args* args, void* stream);
 
+/* ---- backward (the reference has none: gpu/triton_attn.py:9-10, README.md:118) ------
+ * pa_index_transpose: for each of the nk key blocks, the query blocks whose list
+ * (kv_idx / kv_num / kv_partial of an index built at BQ = A, pitch columns) holds it, in
+ * ascending order, with the partial flag: q_num [nk], q_idx / q_partial [nk, tpitch].
+ * With q_idx NULL only q_num is written (size tpitch as max q_num, then call again).
+ *
+ * pa_attn_bwd: gradients of o = softmax(scale q k^T masked) v for f16 / bf16, D = 64
+ * or 128, N a multiple of 64, from the forward's lse (natural log, [BH, N], row stride
+ * lse_sb; -inf rows get no gradient) and dO.  q, k, v, o, dout, dq, dk, dv are
+ * [BH, N, D] with the same element strides sb / sn.  The index is the forward's at
+ * BQ = A = 64 and its transpose; the mask is evaluated on partial tiles only, at
+ * (perm_q[r], perm_kv[c]) when the tables are given (tensors stay in index space).
+ * dvec is a caller-owned fp32 [BH, N] workspace (rowsum(dO * O), same stride as lse). */
+int pa_index_transpose(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial, int32_t nq,
+                       int64_t pitch, int32_t nk, int32_t* q_num, int32_t* q_idx, int8_t* q_partial,
+                       int64_t tpitch, void* stream);
+
+typedef struct pa_attn_bwd_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  int64_t sb, sn;
+  const float* lse;
+  float* dvec;
+  int64_t lse_sb;
+  int64_t BH, N;
+  int32_t D, dtype;
+  float scale;
+  const int32_t* kv_idx;
+  const int32_t* kv_num;
+  const int8_t* kv_partial;
+  int64_t pitch;
+  const int32_t* q_idx;
+  const int32_t* q_num;
+  const int8_t* q_partial;
+  int64_t tpitch;
+  pa_mask mask;
+} pa_attn_bwd_args;
+
+int pa_attn_bwd(const pa_attn_bwd_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,8 @@ softmax, rows with no live key -> 0, @ V -- in float64 numpy, row-chunked (exact
 softmax is per row), with the per-row log-sum-exp.  online_softmax: the kernel's
 tile recurrence as tests/test_kernel_math.py:27-48 restates _attn_fwd (finite
 sentinel, l > 0 guard).  lse_merge: the log-sum-exp combine of a disjoint split.
+dense_attention_bwd: the textbook gradient of that softmax attention (the reference
+has no backward); pinned against torch.autograd in tests/test_oracle_backward.py.
 """
 import numpy as np
 
@@ -95,3 +97,35 @@ def dense_attention_torch(q, k, v, mask_rows, scale=None, row_chunk=1024):
         p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
         out[:, r0:r1] = p @ vf
     return out
+
+
+def dense_attention_bwd(q, k, v, do, mask_rows, scale=None, row_chunk=256, dtype=np.float64):
+    """Gradients of o = softmax(scale q k^T, masked) v with respect to q, k, v for an
+    upstream gradient do: with P the masked softmax (rows with no live key: P = 0),
+    dV = P^T dO, dP = dO V^T, dS = P (dP - rowsum(dO o)), dQ = scale dS K,
+    dK = scale dS^T Q.  q, do: [BH, Nq, D]; k, v: [BH, Nk, D]; mask_rows(r0, r1) ->
+    bool [r1 - r0, Nk].  Returns (dq, dk, dv) in `dtype`."""
+    BH, N, D = q.shape
+    scale = scale or D ** -0.5
+    qf, kf, vf, gf = (np.asarray(x, dtype=dtype) for x in (q, k, v, do))
+    dq = np.zeros_like(qf)
+    dk = np.zeros_like(kf)
+    dv = np.zeros_like(vf)
+    for r0 in range(0, N, row_chunk):
+        r1 = min(N, r0 + row_chunk)
+        m = mask_rows(r0, r1)
+        s = np.einsum("bqd,bkd->bqk", qf[:, r0:r1], kf) * scale
+        s = np.where(m[None], s, -np.inf)
+        mx = s.max(axis=-1, keepdims=True)
+        mx = np.where(np.isfinite(mx), mx, 0.0)
+        e = np.exp(s - mx)
+        den = e.sum(axis=-1, keepdims=True)
+        p = np.where(den > 0, e / np.where(den > 0, den, 1.0), 0.0)
+        o = np.einsum("bqk,bkd->bqd", p, vf)
+        g = gf[:, r0:r1]
+        dv += np.einsum("bqk,bqd->bkd", p, g)
+        dp = np.einsum("bqd,bkd->bqk", g, vf)
+        ds = p * (dp - (g * o).sum(axis=-1, keepdims=True))
+        dq[:, r0:r1] = scale * np.einsum("bqk,bkd->bqd", ds, kf)
+        dk += scale * np.einsum("bqk,bqd->bkd", ds, qf[:, r0:r1])
+    return dq, dk, dv

@@ -1,0 +1,117 @@
+"""Backward of the block-sparse attention (pa_attn_bwd, pa_index_transpose) against the
+float64 oracle gradient (oracle.attention.dense_attention_bwd, itself pinned against
+torch.autograd): the textbook gradient of gpu/reference.py:5-17's attention, which the
+reference does not implement.  The kernel takes the forward's o (in the input dtype)
+and lse; the tolerance is on the error relative to the largest reference gradient."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import masks as om
+from oracle import permute as op
+from polyhedral_amd import attention as pattn
+from polyhedral_amd import backward as pbwd
+from polyhedral_amd import index as pindex
+from polyhedral_amd.polyattn import masks as pm
+from polyhedral_amd.registry import numpy_mask, triton_params
+from tests.util import as64, make_qkv
+
+pytestmark = pytest.mark.gpu
+
+# max |got - want| / max |want| per gradient
+REL = {torch.bfloat16: 3e-2, torch.float16: 5e-3}
+
+
+def _rel_err(got, want):
+    return float(np.abs(as64(got) - want).max() / max(np.abs(want).max(), 1e-6))
+
+
+def _oracle(q, k, v, do, rows):
+    o, lse = oatt.dense_attention(as64(q), as64(k), as64(v), rows)
+    grads = oatt.dense_attention_bwd(as64(q), as64(k), as64(v), as64(do), rows)
+    return o, lse, grads
+
+
+def _check(grads, want, dtype, what):
+    for g, w_, nm in zip(grads, want, ("dq", "dk", "dv")):
+        e = _rel_err(g, w_)
+        assert e < REL[dtype], f"{what} {nm}: relative error {e:.3e}"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("name", ["causal", "window-128", "dilated-8", "band256+lat16", "sinks4+win256",
+                                  "local256+str8", "prefixlm-2048"])
+def test_gradients_equal_oracle(gpu, name, dtype, D):
+    BH, N = 2, 1024
+    q, k, v = make_qkv(BH, N, D, dtype, seed=D)
+    do = make_qkv(BH, N, D, dtype, seed=D + 1)[0]
+    rows = oatt.spec_rows(om.NAMED[name], N)
+    o, lse, want = _oracle(q, k, v, do, rows)
+    plan = pbwd.BackwardPlan(numpy_mask(name), N, gpu)
+    dev = lambda x: x.to(gpu)
+    grads = plan.backward(dev(q), dev(k), dev(v), torch.from_numpy(o).to(dtype).to(gpu),
+                          torch.from_numpy(lse).float().to(gpu), dev(do))
+    _check(grads, want, dtype, f"{name} {dtype} D={D}")
+
+
+def test_forward_then_backward(gpu):
+    """The streaming forward's o and lse feed the backward."""
+    BH, N, D, name = 2, 2048, 128, "band256+lat16"
+    q, k, v = make_qkv(BH, N, D, torch.bfloat16, seed=3)
+    do = make_qkv(BH, N, D, torch.bfloat16, seed=4)[0]
+    qd, kd, vd, dod = (x.to(gpu) for x in (q, k, v, do))
+    lse = torch.empty(BH, N, device=gpu)
+    bi = pindex.build(numpy_mask(name), N, 128, 32)
+    launch = pattn.prepare(qd, kd, vd, *pindex.to_cuda(bi, gpu), *triton_params(name), 128, 32, lse=lse)
+    with torch.cuda.device(gpu):
+        o = launch()
+    grads = pbwd.BackwardPlan(numpy_mask(name), N, gpu).backward(qd, kd, vd, o, lse, dod)
+    _, _, want = _oracle(q, k, v, do, oatt.spec_rows(om.NAMED[name], N))
+    _check(grads, want, torch.bfloat16, "forward + backward")
+
+
+def test_permuted_basis_gives_the_permuted_gradients(gpu):
+    """Tensors relabelled by rp8 with the mask evaluated through the permutation: the
+    gradients are the identity-basis gradients relabelled."""
+    BH, N, D, name = 2, 1024, 64, "dilated-8"
+    q, k, v = make_qkv(BH, N, D, torch.float16, seed=5)
+    do = make_qkv(BH, N, D, torch.float16, seed=6)[0]
+    p = op.residue_perm(N, 8)
+    rows = oatt.spec_rows(om.NAMED[name], N)
+    o, lse, want = _oracle(q, k, v, do, rows)
+    pt = torch.from_numpy(p).long()
+    plan = pbwd.BackwardPlan(numpy_mask(name), N, gpu, perm=p)
+    grads = plan.backward(*(x[:, pt].contiguous().to(gpu) for x in (q, k, v)),
+                          torch.from_numpy(o).to(torch.float16)[:, pt].contiguous().to(gpu),
+                          torch.from_numpy(lse).float()[:, pt].contiguous().to(gpu), do[:, pt].contiguous().to(gpu))
+    inv = torch.from_numpy(np.argsort(p)).long()
+    _check([g.cpu()[:, inv] for g in grads], want, torch.float16, "rp8 basis")
+    # the permuted basis lists fewer tiles
+    assert int(plan.kv_num.sum()) < int(pbwd.BackwardPlan(numpy_mask(name), N, gpu).kv_num.sum())
+
+
+def test_dead_rows_and_transposed_index(gpu):
+    BH, N, D = 1, 512, 128
+    M = om.dense(om.NAMED["window-128"], N)
+    M[70] = False
+    q, k, v = make_qkv(BH, N, D, torch.bfloat16, seed=7)
+    do = make_qkv(BH, N, D, torch.bfloat16, seed=8)[0]
+    o, lse, want = _oracle(q, k, v, do, lambda a, b: M[a:b])
+    plan = pbwd.BackwardPlan(pm.DenseMask(M), N, gpu)
+    grads = plan.backward(q.to(gpu), k.to(gpu), v.to(gpu), torch.from_numpy(o).to(torch.bfloat16).to(gpu),
+                          torch.from_numpy(lse).float().to(gpu), do.to(gpu))
+    assert torch.count_nonzero(grads[0][0, 70]) == 0
+    _check(grads, want, torch.bfloat16, "dense mask with a dead row")
+    # the transpose lists, per key block, exactly the query blocks holding it
+    kv_idx, kv_num = plan.kv_idx.cpu().numpy(), plan.kv_num.cpu().numpy()
+    kv_part = plan.kv_partial.cpu().numpy()
+    q_idx, q_num, q_part = (t.cpu().numpy() for t in (plan.q_idx, plan.q_num, plan.q_partial))
+    nb = N // 64
+    for kb in range(nb):
+        holders = [(qb, kv_part[qb, list(kv_idx[qb, :kv_num[qb]]).index(kb)]) for qb in range(nb)
+                   if kb in kv_idx[qb, :kv_num[qb]]]
+        assert q_num[kb] == len(holders)
+        assert [int(x) for x in q_idx[kb, :q_num[kb]]] == [h[0] for h in holders]
+        assert [int(x) for x in q_part[kb, :q_num[kb]]] == [int(h[1]) for h in holders]
