@@ -201,6 +201,53 @@ def measure_decode(wl, q, k, v, residues=(0, 16), reps=200, warmup=20):
                 "HIP graph replay; algorithmic bytes = live K/V rows + appended rows + q + o", **out)
 
 
+def measure_backward(wl, q, k, v, residue, reps=20, warmup=5):
+    """The backward of the workload's whole mask in one pass (pa_attn_bwd: pre-pass, dK/dV
+    and dQ kernels over 64 x 64 tiles) in the residue-`residue` basis (0: identity), the
+    tensors relabelled before the timed region.  Live FLOP = 8 D per live pair and head
+    (dV, dP, dQ, dK; the recomputed scores are not counted)."""
+    import torch
+
+    from polyhedral_amd import attention as pattn
+    from polyhedral_amd import backward as pbwd
+    from polyhedral_amd import index as pindex
+    from polyhedral_amd.perm import residue_perm
+    from polyhedral_amd.spec import device_mask
+    H, L, D = wl.H, wl.L, wl.D
+    p = residue_perm(L, residue) if residue else None
+    pt = torch.from_numpy(p).long().to(q.device) if p is not None else None
+    qp, kp, vp = ((x[:, pt].contiguous() if pt is not None else x) for x in (q, k, v))
+    dop = torch.randn(qp.shape, generator=torch.Generator().manual_seed(7)).to(q.dtype).to(q.device)
+    # o and lse from this build's forward on the same (relabelled) tensors
+    lse = torch.empty(H, L, dtype=torch.float32, device=q.device)
+    bi = pindex.build(wl.union, L, 64, 64, perm=p, device=q.device)
+    launch = pattn.prepare(qp, kp, vp, *pindex.to_cuda(bi, q.device),
+                           device_mask(wl.union, L, q.device, perm=p), 0, 0, 0, 64, 64, lse=lse,
+                           kernel="general")
+    o = launch()
+    plan = pbwd.BackwardPlan(wl.union, L, q.device, perm=p)
+    for _ in range(warmup):
+        plan.backward(qp, kp, vp, o, lse, dop)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for _ in range(reps):
+        plan.backward(qp, kp, vp, o, lse, dop)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    live = int(bi.live)
+    tiles = int(plan.kv_num.sum())
+    fl = 8 * D * live * H
+    tf = fl / (ms * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[_dt(q.dtype)]
+    return dict(basis=f"rp{residue}" if residue else "identity", tile=64, tiles=tiles, ms=round(ms, 4),
+                live_tflops=round(tf, 2), tile_tflops=round(8 * D * tiles * 64 * 64 * H / (ms * 1e-3) / 1e12, 2),
+                roofline=dict(bound="mfma", achieved=round(tf, 2), peak=peak, unit="TFLOP/s", frac=round(tf / peak, 4)),
+                note="one backward of the whole mask (pre-pass + dK/dV + dQ launches); live FLOP = 8 D per live "
+                     "pair and head, recomputed scores not counted")
+
+
 def cpu_baseline(wl, budget_s=12.0):
     """Oracle dense fp32 attention on the host over (head, 1024-row chunk) units in
     order until the budget is spent; live-FLOP TFLOP/s over what was processed."""
@@ -289,6 +336,8 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     permute = measure_permute(q, k, v, residues[0]) if residues and variant is None else None
     decode = (measure_decode(wl, q, k, v, (0,) + tuple(sorted(set(residues))))
               if variant is None and wl.D in (64, 128) and wl.dtype != torch.float32 else None)
+    backward = (measure_backward(wl, q, k, v, max(residues) if residues else 0)
+                if variant is None and wl.D in (64, 128) and wl.dtype != torch.float32 and wl.L % 64 == 0 else None)
     kernels = ["attn_stream_kernel" if x.kernel == "stream" else "attn_fwd_kernel" for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
     for i, bi in enumerate(plan.launched):
@@ -323,6 +372,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
                                     "memory-side cache)")
     res["permute"] = permute
     res["decode"] = decode
+    res["backward"] = backward
     res["_launches"] = len(launches)
     if with_cpu:
         log(f"[bench] cpu baseline for {name} ...")
@@ -388,6 +438,10 @@ def main():
                     log("[bench]   decode (append + attend, 1 token): " + ", ".join(
                         f"{b} {dd[b]['ms_per_token'] * 1e3:.1f} us ({dd[b]['gb_per_s']:.0f} GB/s)"
                         for b in dd if isinstance(dd[b], dict)))
+                if r.get("backward"):
+                    bw = r["backward"]
+                    log(f"[bench]   backward ({bw['basis']}, 64x64, {bw['tiles']} tiles): {bw['ms']:.3f} ms, "
+                        f"{bw['live_tflops']:.0f} live TFLOP/s ({100 * bw['roofline']['frac']:.1f}%)")
                 if r.get("permute"):
                     pm_ = r["permute"]
                     log(f"[bench]   permute rp{pm_['residue']}: Q/K/V gather {pm_['gather_qkv']['gb_per_s']:.0f} GB/s, "
@@ -420,6 +474,7 @@ def main():
         isolated=r["isolated"],
         permute=r["permute"],
         decode=r["decode"],
+        backward=r["backward"],
     )
     print(json.dumps(line), flush=True)
 

@@ -82,18 +82,24 @@ constexpr int npitch() { return D * (int)sizeof(T) + 16; }
 template <typename T, int D>
 constexpr int tpitch() { return D * (int)sizeof(T) + 64; }
 
-// Stage rows r0 .. r0 + 63 of a [BH, N, D] tensor into LDS at both pitches (dst_n may
-// equal nullptr to skip one).  128 threads, 16 bytes each per pass.
-template <typename T, int D>
+// Stage rows r0 .. r0 + 63 of a [BH, N, D] tensor into LDS at the row-read pitch and,
+// with TR, also at the transposed-read pitch.  128 threads; a fixed unit count per
+// thread, so every load is issued before any store.
+template <typename T, int D, bool TR>
 __device__ __forceinline__ void stage_tile(const char* base, int64_t sn, int r0, char* dst_n, char* dst_t, int tid) {
   constexpr int UPR = D * (int)sizeof(T) / 16;
-  constexpr int UNITS = kBT * UPR;
+  constexpr int PER = kBT * UPR / 128;
+  uint4 x[PER];
 #pragma unroll
-  for (int u = tid; u < UNITS; u += 128) {
-    const int r = u / UPR, c = u - (u / UPR) * UPR;
-    const uint4 x = *reinterpret_cast<const uint4*>(base + ((int64_t)(r0 + r) * sn) * (int64_t)sizeof(T) + 16 * c);
-    if (dst_n) *reinterpret_cast<uint4*>(dst_n + r * npitch<T, D>() + 16 * c) = x;
-    if (dst_t) *reinterpret_cast<uint4*>(dst_t + r * tpitch<T, D>() + 16 * c) = x;
+  for (int i = 0; i < PER; ++i) {
+    const int u = tid + 128 * i, r = u / UPR, c = u % UPR;
+    x[i] = *reinterpret_cast<const uint4*>(base + ((int64_t)(r0 + r) * sn) * (int64_t)sizeof(T) + 16 * c);
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int u = tid + 128 * i, r = u / UPR, c = u % UPR;
+    *reinterpret_cast<uint4*>(dst_n + r * npitch<T, D>() + 16 * c) = x[i];
+    if constexpr (TR) *reinterpret_cast<uint4*>(dst_t + r * tpitch<T, D>() + 16 * c) = x[i];
   }
 }
 
@@ -135,6 +141,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1))) void b
   __shared__ __attribute__((aligned(16))) char do_n[kBT * NP];
   __shared__ __attribute__((aligned(16))) char do_t[kBT * TP];
   __shared__ float lse_s[kBT], dvec_s[kBT];
+  __shared__ int32_t qo_s[kBT];
+  __shared__ pa_term terms_s[PA_MAX_TERMS];
+#pragma unroll
+  for (int i = 0; i < PA_MAX_TERMS; ++i)  // (constant indices into the argument block)
+    if (threadIdx.x == i) terms_s[i] = a.pred.terms[i];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, G = lane >> 5, m = lane & 31;
   const int kb = blockIdx.x;
@@ -156,12 +167,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1))) void b
     const int qb = a.q_idx[(int64_t)kb * a.tpitch + t];
     const bool partial = a.q_partial[(int64_t)kb * a.tpitch + t] != 0;
     __syncthreads();  // the previous block's tiles are consumed
-    stage_tile<T, D>(hq, a.sn, qb * kBT, q_n, q_t, tid);
-    stage_tile<T, D>(hdo, a.sn, qb * kBT, do_n, do_t, tid);
+    stage_tile<T, D, true>(hq, a.sn, qb * kBT, q_n, q_t, tid);
+    stage_tile<T, D, true>(hdo, a.sn, qb * kBT, do_n, do_t, tid);
     if (tid < kBT) {
       const float l = a.lse[bh * a.lse_sb + qb * kBT + tid];
       lse_s[tid] = l * 1.4426950408889634f;
       dvec_s[tid] = a.dvec[bh * a.lse_sb + qb * kBT + tid];
+      qo_s[tid] = orig_of(a.pred.perm_q, qb * kBT + tid);
     }
     __syncthreads();
 #pragma unroll
@@ -176,14 +188,25 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1))) void b
         s = Mma<T>::mma(__builtin_bit_cast(Frag, *reinterpret_cast<const uint4*>(qrow + kc * 32)), kf[kc], s);
         dp = Mma<T>::mma(__builtin_bit_cast(Frag, *reinterpret_cast<const uint4*>(drow + kc * 32)), vf[kc], dp);
       }
+      // live bit i of the lane's elements: all set on a full tile, one rolled copy of the
+      // predicate (terms from LDS) on a partial one
+      uint32_t live = 0xffffu;
+      if (partial) {
+        live = 0u;
+#pragma unroll 1
+        for (int i = 0; i < 16; ++i) {
+          const int qr = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
+          if (pred_live_rolled(terms_s, a.pred.n_include, a.pred.n_exclude, qo_s[qr], key_o, a.pred.dense_bits,
+                               a.pred.dense_words))
+            live |= 1u << i;
+        }
+      }
       float p[16], ds[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int qr = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
-        bool live = true;
-        if (partial) live = pred_live(a.pred, orig_of(a.pred.perm_q, qb * kBT + qr), key_o);
         const float l2 = lse_s[qr];
-        p[i] = (live && l2 != -INFINITY) ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], a.c, -l2)) : 0.f;
+        p[i] = (((live >> i) & 1u) && l2 != -INFINITY) ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], a.c, -l2)) : 0.f;
         ds[i] = p[i] * (dp[i] - dvec_s[qr]);
       }
 #pragma unroll
@@ -233,6 +256,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void b
   __shared__ __attribute__((aligned(16))) char k_t[kBT * TP];
   __shared__ __attribute__((aligned(16))) char v_n[kBT * NP];
   __shared__ int32_t ko_s[kBT];
+  __shared__ pa_term terms_s[PA_MAX_TERMS];
+#pragma unroll
+  for (int i = 0; i < PA_MAX_TERMS; ++i)
+    if (threadIdx.x == i) terms_s[i] = a.pred.terms[i];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, G = lane >> 5, m = lane & 31;
   const int qb = blockIdx.x;
@@ -256,8 +283,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void b
     const int kb = a.kv_idx[(int64_t)qb * a.pitch + t];
     const bool partial = a.kv_partial[(int64_t)qb * a.pitch + t] != 0;
     __syncthreads();
-    stage_tile<T, D>(hk, a.sn, kb * kBT, k_n, k_t, tid);
-    stage_tile<T, D>(hv, a.sn, kb * kBT, v_n, nullptr, tid);
+    stage_tile<T, D, true>(hk, a.sn, kb * kBT, k_n, k_t, tid);
+    stage_tile<T, D, false>(hv, a.sn, kb * kBT, v_n, nullptr, tid);
     if (tid < kBT) ko_s[tid] = orig_of(a.pred.perm_kv, kb * kBT + tid);
     __syncthreads();
 #pragma unroll
@@ -272,13 +299,22 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void b
         s = Mma<T>::mma(__builtin_bit_cast(Frag, *reinterpret_cast<const uint4*>(krow + kc * 32)), qf[kc], s);
         dp = Mma<T>::mma(__builtin_bit_cast(Frag, *reinterpret_cast<const uint4*>(vrow + kc * 32)), df[kc], dp);
       }
+      uint32_t live = 0xffffu;
+      if (partial) {
+        live = 0u;
+#pragma unroll 1
+        for (int i = 0; i < 16; ++i) {
+          const int kr = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
+          if (pred_live_rolled(terms_s, a.pred.n_include, a.pred.n_exclude, q_o, ko_s[kr], a.pred.dense_bits,
+                               a.pred.dense_words))
+            live |= 1u << i;
+        }
+      }
       float ds[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int kr = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
-        bool live = true;
-        if (partial) live = pred_live(a.pred, q_o, ko_s[kr]);
-        const float p = (live && l2 != -INFINITY) ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], a.c, -l2)) : 0.f;
+        const float p =
+            (((live >> i) & 1u) && l2 != -INFINITY) ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], a.c, -l2)) : 0.f;
         ds[i] = p * (dp[i] - dr);
       }
 #pragma unroll
