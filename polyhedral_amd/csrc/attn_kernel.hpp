@@ -182,6 +182,25 @@ __device__ __forceinline__ s16x4 lds_read_tr(const char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
 }
 
+typedef __attribute__((address_space(3))) char lds_char_t;
+typedef const __attribute__((address_space(3))) char* lds_cptr;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef const __attribute__((address_space(3))) u32x4 lds_u4;
+typedef const __attribute__((address_space(3))) uint32_t lds_u32;
+
+// LDS DMA (global_load_lds_dwordx4 / _dword): lane l writes LDS[m0 + 16 l] / LDS[m0 + 4 l]
+// from gbase + voff.  Issued from inline assembly, so the compiler, which cannot tell
+// which LDS bytes a DMA writes, does not wait for it before unrelated LDS reads; the
+// caller waits itself (dma_wait_all, then a work-group barrier).
+__device__ __forceinline__ void dma_x4(uint32_t m0, const char* gbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+}
+__device__ __forceinline__ void dma_x1(uint32_t m0, const char* gbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+}
+__device__ __forceinline__ void dma_wait_all() { asm volatile("s_waitcnt vmcnt(0)"); }
+
 // Uniform description of the 4 segments (16 index-space KV rows each) of one step.
 struct StepMeta {
   int32_t base[4];   // index-space KV row of the segment's first row; -1 past the list

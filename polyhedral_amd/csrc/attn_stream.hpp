@@ -39,13 +39,6 @@ struct StepDesc {
 };
 static_assert(sizeof(StepDesc) == 64, "descriptor is 16 words");
 
-typedef __attribute__((address_space(3))) char lds_char_t;
-typedef const __attribute__((address_space(3))) char* lds_cptr;
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef const __attribute__((address_space(3))) u32x4 lds_u4;
-typedef const __attribute__((address_space(3))) uint32_t lds_u32;
-
 // LDS layout: two bitmap slots (4 x 128 words each), a ring of two V slots and a ring of
 // two K slots (64 rows x 256 B each).  K and V have separate rings because a step's
 // K is consumed one iteration before its V (the QK of step j + 1 runs beside the P.V
@@ -57,15 +50,6 @@ constexpr int kVring = 4096;
 constexpr int kKring = 36864;
 constexpr int kSlot = 16384;
 constexpr int kStreamSmem = kKring + 2 * kSlot;
-
-// LDS DMA of 16 bytes per lane (lane l writes LDS[m0 + 16 l]) / 4 bytes per lane.
-__device__ __forceinline__ void dma_x4(uint32_t m0, const char* gbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
-}
-__device__ __forceinline__ void dma_x1(uint32_t m0, const char* gbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
-}
-__device__ __forceinline__ void dma_wait_all() { asm volatile("s_waitcnt vmcnt(0)"); }
 
 template <typename T>
 __device__ __forceinline__ float dot2_sum(uint32_t packed, float acc);

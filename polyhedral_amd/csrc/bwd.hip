@@ -21,6 +21,8 @@
 // perm_kv map index-space rows to them, as in the forward).
 #include <math.h>
 
+#include <type_traits>
+
 #include "attn_kernel.hpp"
 
 namespace pa {
@@ -342,6 +344,508 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void b
   }
 }
 
+// ---------------------------------------------------------------------------------
+// D = 128 (f16 / bf16): the same two products per tile, with the staged tiles brought
+// into LDS by LDS DMA (no staging registers, no LDS stores), two stages deep: the next
+// listed tile moves while the current one is consumed, behind one wait and one barrier
+// per tile.  A DMA instruction writes 64 consecutive 16-byte units, so the rows are
+// stored unpadded (256 B) and one XOR swizzle of the 16-byte units serves both ways a
+// tile is read: unit u of row r sits at u ^ bswz(r), bswz(r) = 4 (r % 4) + (r / 4) % 4.
+// The 16 rows of a 16-byte row read land on 16 different units of the 256-byte bank
+// window, and the 4 rows of a transposed read on 4 different 64-byte groups.
+// LDS: two stages of two tiles, then per stage 1 KB of row vectors (lse, rowsum(dO O),
+// original row numbers), then the mask terms.
+constexpr int kTB = kBT * 256;
+constexpr int kStage = 2 * kTB;
+constexpr int kVecOff = 2 * kStage;
+constexpr int kTermsOff = kVecOff + 2 * 1024;
+constexpr int kBwdSmem = kTermsOff + PA_MAX_TERMS * (int)sizeof(pa_term);
+
+typedef const __attribute__((address_space(3))) f32x4 lds_f4;
+typedef const __attribute__((address_space(3))) int32_t lds_i32;
+typedef const __attribute__((address_space(4))) int32_t cint;
+typedef const __attribute__((address_space(4))) int8_t cbyte;
+
+__device__ __forceinline__ int bswz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+
+// Per-lane LDS geometry of a staged tile (offsets of stage, tile, block and chunk are
+// immediates on top of these).
+struct TileReads {
+  lds_cptr row[8];     // 16-byte row reads: row m, unit 2 kc + G
+  lds_cptr tr[4][2];   // transposed reads of block db: rows 4 G + j16 / 4 (+8)
+};
+
+__device__ __forceinline__ TileReads tile_reads(lds_cptr lds, int lane) {
+  TileReads t;
+  const int m = lane & 31, G = lane >> 5, j16 = lane & 15, h16 = (lane >> 4) & 1;
+#pragma unroll
+  for (int kc = 0; kc < 8; ++kc) {
+    t.row[kc] = lds + m * 256 + 16 * ((2 * kc + G) ^ bswz(m));
+    // (opaque, so each address stays whole in one register)
+    asm volatile("" : "+v"(t.row[kc]));
+  }
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int R = 4 * G + (j16 >> 2) + 8 * s;
+      const int u = 4 * db + 2 * h16 + ((j16 & 3) >> 1);
+      t.tr[db][s] = lds + R * 256 + 16 * (u ^ bswz(R)) + 8 * (j16 & 1);
+      asm volatile("" : "+v"(t.tr[db][s]));
+    }
+  return t;
+}
+
+// A operand X^T of rows r0 .. r0 + 15 (r0 a multiple of 16) of a staged tile at byte
+// offset `off` (stage + tile + r0 * 256): the transposed product's fragment for block db.
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::frag tr_frag_sw(const TileReads& t, int db, int off) {
+  const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t.tr[db][0] + off));
+  const s16x4 x2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t.tr[db][1] + off));
+  const uint4 vx = {__builtin_bit_cast(uint2, x1).x, __builtin_bit_cast(uint2, x1).y, __builtin_bit_cast(uint2, x2).x,
+                    __builtin_bit_cast(uint2, x2).y};
+  return __builtin_bit_cast(typename Mma<T>::frag, vx);
+}
+
+// DMA of rows r0 .. r0 + 63 of two [N, 128] tensors (row pitch rowb bytes, heads already
+// applied) into stage tiles at LDS m0 and m0 + kTB.  Wave w moves rows 32 w .. 32 w + 31;
+// its instruction i writes rows 32 w + 4 i + l / 16, lane l unit l % 16, fetching the
+// unit the swizzle stores there: (l % 16) ^ (4 (l / 16) + i % 4) (dvoff[i % 4]).
+__device__ __forceinline__ void dma_tile_pair(uint32_t m0, const char* g0, const char* g1, int64_t rowb, int64_t r0,
+                                              int w, const uint32_t* dvoff) {
+  const char* a0 = g0 + (r0 + 32 * w) * rowb;
+  const char* a1 = g1 + (r0 + 32 * w) * rowb;
+  const uint32_t mw = m0 + (uint32_t)(32 * w * 256);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    dma_x4(mw + i * 1024, a0 + 4 * i * rowb, dvoff[i & 3]);
+    dma_x4(mw + kTB + i * 1024, a1 + 4 * i * rowb, dvoff[i & 3]);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_dkdv_stream_kernel(const BwdK a) {
+  using Frag = typename Mma<T>::frag;
+  constexpr int ESZ = 2, NKC = 8, NDB = 4;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char_t*)smem;
+  lds_cptr lds = (lds_cptr)smem;
+  pa_term* terms_s = reinterpret_cast<pa_term*>(smem + kTermsOff);
+#pragma unroll
+  for (int i = 0; i < PA_MAX_TERMS; ++i)  // (constant indices into the argument block)
+    if (threadIdx.x == i) terms_s[i] = a.pred.terms[i];
+
+  const int tid = threadIdx.x, lane = tid & 63, G = lane >> 5, m = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // consecutive key blocks of a head on one XCD: neighbours share their query tiles in L2
+  const int64_t id = xcd_remap(blockIdx.x, (int64_t)gridDim.x);
+  const int kb = (int)(id % a.nb);
+  const int64_t bh = id / a.nb;
+  const int key = kb * kBT + w * 32 + m;
+  const int key_o = orig_of(a.pred.perm_kv, key);
+  const int64_t rowb = a.sn * ESZ;
+  const char* hq = a.q + bh * a.sb * ESZ;
+  const char* hdo = a.dout + bh * a.sb * ESZ;
+  const char* hlse = reinterpret_cast<const char*>(a.lse + bh * a.lse_sb);
+  const char* hdvec = reinterpret_cast<const char*>(a.dvec + bh * a.lse_sb);
+  const char* hperm = reinterpret_cast<const char*>(a.pred.perm_q);
+
+  uint32_t dvoff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    dvoff[j] = (uint32_t)((lane >> 4) * rowb) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
+  // query block qb into stage S: Q and dO tiles; lse (and the original row numbers) by
+  // wave 0, rowsum(dO O) by wave 1
+  auto dma = [&](int qb, int S) __attribute__((always_inline)) {
+    dma_tile_pair(lds0 + S * kStage, hq, hdo, rowb, (int64_t)qb * kBT, w, dvoff);
+    const uint32_t mv = lds0 + kVecOff + S * 1024;
+    if (w == 0) {
+      dma_x1(mv, hlse + (int64_t)qb * 256, 4u * lane);
+      if (hperm) dma_x1(mv + 512, hperm + (int64_t)qb * 256, 4u * lane);
+    } else {
+      dma_x1(mv + 256, hdvec + (int64_t)qb * 256, 4u * lane);
+    }
+  };
+
+  const TileReads rd = tile_reads(lds, lane);
+  lds_cptr vrow = lds + kVecOff + 16 * G;  // lse of rows 8 j + 4 G + 0..3 (+ 32 lb)
+
+  Frag kf[NKC], vf[NKC];
+  row_frags<T, 128>(a.k + (bh * a.sb + (int64_t)key * a.sn) * ESZ + 16 * G, kf);
+  row_frags<T, 128>(a.v + (bh * a.sb + (int64_t)key * a.sn) * ESZ + 16 * G, vf);
+  f32x16 dkt[NDB], dvt[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) dkt[i] = dvt[i] = f32x16{0};
+
+  // One tile (stage S): four phases in one straight-line block, the order spelled out for
+  // the scheduler (left alone it waits on every LDS read):
+  //   A  S = Q K^T, dP = dO V^T of query rows 0..31;
+  //   B  the same for rows 32..63, beside the gradient of the scores of rows 0..31;
+  //   C  dV^T += dO^T P, dK^T += Q^T dS of rows 0..31, beside the scores' gradient of 32..63;
+  //   D  dV^T, dK^T of rows 32..63.
+  // Element i of a score block is query row 32 lb + 8 (i / 4) + 4 G + i % 4, key `key`.
+  auto compute = [&](auto SC, bool partial, int qb) __attribute__((always_inline)) {
+    constexpr int S = decltype(SC)::value;
+    constexpr int SO = S * kStage;
+    uint32_t live[2] = {0xffffu, 0xffffu};
+    if (partial) {
+      lds_i32* qo = (lds_i32*)(lds + kVecOff + S * 1024 + 512);
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb) {
+        live[lb] = 0u;
+#pragma unroll 1
+        for (int i = 0; i < 16; ++i) {
+          const int qr = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
+          const int q_o = hperm ? qo[qr] : qb * kBT + qr;
+          if (pred_live_rolled(terms_s, a.pred.n_include, a.pred.n_exclude, q_o, key_o, a.pred.dense_bits,
+                               a.pred.dense_words))
+            live[lb] |= 1u << i;
+        }
+      }
+    }
+    // scores of rows 32 lb .. +31
+    auto scores = [&](int lb, f32x16& s, f32x16& dp) __attribute__((always_inline)) {
+      u32x4 qa[NKC], da[NKC];
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        qa[kc] = *(lds_u4*)(rd.row[kc] + SO + lb * 8192);
+        da[kc] = *(lds_u4*)(rd.row[kc] + SO + kTB + lb * 8192);
+      }
+      s = Mma<T>::mma(__builtin_bit_cast(Frag, qa[0]), kf[0], f32x16{0});
+      dp = Mma<T>::mma(__builtin_bit_cast(Frag, da[0]), vf[0], f32x16{0});
+#pragma unroll
+      for (int kc = 1; kc < NKC; ++kc) {
+        s = Mma<T>::mma(__builtin_bit_cast(Frag, qa[kc]), kf[kc], s);
+        dp = Mma<T>::mma(__builtin_bit_cast(Frag, da[kc]), vf[kc], dp);
+      }
+    };
+    // P and dS of rows 32 lb .. +31 as MFMA operands (chunks of 16 rows)
+    auto grads = [&](int lb, const f32x16& s, const f32x16& dp, Frag* pf, Frag* sf) __attribute__((always_inline)) {
+      f32x4 l4[4], d4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        l4[j] = *(lds_f4*)(vrow + S * 1024 + (32 * lb + 8 * j) * 4);
+        d4[j] = *(lds_f4*)(vrow + S * 1024 + 256 + (32 * lb + 8 * j) * 4);
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        f32x8 pv, sv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 8 * c + e;
+          const float lse = l4[i >> 2][i & 3];
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], a.c, -lse * 1.4426950408889634f));
+          const float p = (((live[lb] >> i) & 1u) && lse != -INFINITY) ? pe : 0.f;
+          pv[e] = p;
+          sv[e] = p * (dp[i] - d4[i >> 2][i & 3]);
+        }
+        pf[c] = Mma<T>::cvt(pv);
+        sf[c] = Mma<T>::cvt(sv);
+      }
+    };
+    // dV^T += dO^T P, dK^T += Q^T dS for rows 32 lb .. +31
+    auto accum = [&](int lb, const Frag* pf, const Frag* sf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int off = SO + (32 * lb + 16 * c) * 256;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          dvt[db] = Mma<T>::mma(tr_frag_sw<T>(rd, db, off + kTB), pf[c], dvt[db]);
+          dkt[db] = Mma<T>::mma(tr_frag_sw<T>(rd, db, off), sf[c], dkt[db]);
+        }
+      }
+    };
+    f32x16 s0, dp0, s1, dp1;
+    Frag pf0[2], sf0[2], pf1[2], sf1[2];
+    scores(0, s0, dp0);
+    scores(1, s1, dp1);
+    grads(0, s0, dp0, pf0, sf0);
+    accum(0, pf0, sf0);
+    grads(1, s1, dp1, pf1, sf1);
+    accum(1, pf1, sf1);
+    // A: 4 reads ahead, then one read per MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 12; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    // B: rows 32..63's reads and MFMAs, rows 0..31's gradient in the VALU slots
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 12; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    }
+#pragma unroll
+    for (int q_ = 0; q_ < 4; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    }
+    // C: rows 0..31's accumulation, rows 32..63's gradient in the VALU slots
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 12; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    }
+#pragma unroll
+    for (int q_ = 0; q_ < 4; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    }
+    // D: rows 32..63's accumulation
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 12; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  };
+
+  const int nl = ((cint*)a.q_num)[kb];
+  cint* qlist = (cint*)(a.q_idx + (int64_t)kb * a.tpitch);
+  cbyte* plist = (cbyte*)(a.q_partial + (int64_t)kb * a.tpitch);
+  int qb_c = 0, qb_n = 0;
+  if (nl > 0) {
+    qb_c = qlist[0];
+    dma(qb_c, 0);
+  }
+  if (nl > 1) qb_n = qlist[1];
+  auto step = [&](auto SC, int t) __attribute__((always_inline)) {
+    constexpr int S = decltype(SC)::value;
+    const bool partial = plist[t] != 0;
+    dma_wait_all();
+    __syncthreads();  // stage S is in; every wave is past its reads of stage S ^ 1
+    if (t + 1 < nl) dma(qb_n, S ^ 1);
+    const int qb = qb_c;
+    qb_c = qb_n;
+    if (t + 2 < nl) qb_n = qlist[t + 2];
+    compute(SC, partial, qb);
+  };
+  int t = 0;
+  for (; t + 1 < nl; t += 2) {
+    step(std::integral_constant<int, 0>{}, t);
+    step(std::integral_constant<int, 1>{}, t + 1);
+  }
+  if (t < nl) step(std::integral_constant<int, 0>{}, t);
+
+  // dK^T / dV^T blocks [32 d x 32 keys]: lane (key m, G) holds d = 32 db + 8 i4 + 4 G + 0..3
+  char* dkrow = a.dk + (bh * a.sb + (int64_t)key * a.sn) * ESZ;
+  char* dvrow = a.dv + (bh * a.sb + (int64_t)key * a.sn) * ESZ;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int d0 = 32 * db + 8 * i4 + 4 * G;
+      f32x4 xk = {dkt[db][4 * i4], dkt[db][4 * i4 + 1], dkt[db][4 * i4 + 2], dkt[db][4 * i4 + 3]};
+      const f32x4 xv = {dvt[db][4 * i4], dvt[db][4 * i4 + 1], dvt[db][4 * i4 + 2], dvt[db][4 * i4 + 3]};
+      xk *= a.scale;
+      Mma<T>::store4(dkrow + d0 * ESZ, xk);
+      Mma<T>::store4(dvrow + d0 * ESZ, xv);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_dq_stream_kernel(const BwdK a) {
+  using Frag = typename Mma<T>::frag;
+  constexpr int ESZ = 2, NKC = 8, NDB = 4;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char_t*)smem;
+  lds_cptr lds = (lds_cptr)smem;
+  pa_term* terms_s = reinterpret_cast<pa_term*>(smem + kTermsOff);
+#pragma unroll
+  for (int i = 0; i < PA_MAX_TERMS; ++i)
+    if (threadIdx.x == i) terms_s[i] = a.pred.terms[i];
+
+  const int tid = threadIdx.x, lane = tid & 63, G = lane >> 5, m = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t id = xcd_remap(blockIdx.x, (int64_t)gridDim.x);
+  const int qb = (int)(id % a.nb);
+  const int64_t bh = id / a.nb;
+  const int row = qb * kBT + w * 32 + m;  // this lane's query row (index space)
+  const int q_o = orig_of(a.pred.perm_q, row);
+  const int64_t rowb = a.sn * ESZ;
+  const char* hk = a.k + bh * a.sb * ESZ;
+  const char* hv = a.v + bh * a.sb * ESZ;
+  const char* hperm = reinterpret_cast<const char*>(a.pred.perm_kv);
+
+  uint32_t dvoff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    dvoff[j] = (uint32_t)((lane >> 4) * rowb) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
+  // key block kb into stage S: K and V tiles; the original key numbers by wave 0
+  auto dma = [&](int kb, int S) __attribute__((always_inline)) {
+    dma_tile_pair(lds0 + S * kStage, hk, hv, rowb, (int64_t)kb * kBT, w, dvoff);
+    if (hperm && w == 0) dma_x1(lds0 + kVecOff + S * 1024 + 512, hperm + (int64_t)kb * 256, 4u * lane);
+  };
+
+  const TileReads rd = tile_reads(lds, lane);
+
+  Frag qf[NKC], df[NKC];
+  row_frags<T, 128>(a.q + (bh * a.sb + (int64_t)row * a.sn) * ESZ + 16 * G, qf);
+  row_frags<T, 128>(a.dout + (bh * a.sb + (int64_t)row * a.sn) * ESZ + 16 * G, df);
+  const float lse = a.lse[bh * a.lse_sb + row];
+  const float nl2 = -lse * 1.4426950408889634f;
+  const bool dead = lse == -INFINITY;
+  const float dr = a.dvec[bh * a.lse_sb + row];
+  f32x16 dqt[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) dqt[i] = f32x16{0};
+
+  // One tile (stage S), phases as in the dK/dV kernel: A scores of keys 0..31; B scores of
+  // keys 32..63 beside the gradient of keys 0..31; C dQ^T += K^T dS^T of keys 0..31 beside
+  // the gradient of 32..63; D dQ^T of keys 32..63.  Element i of a score block is key
+  // 32 lb + 8 (i / 4) + 4 G + i % 4, query `row`.
+  auto compute = [&](auto SC, bool partial, int kb) __attribute__((always_inline)) {
+    constexpr int S = decltype(SC)::value;
+    constexpr int SO = S * kStage;
+    uint32_t live[2] = {dead ? 0u : 0xffffu, dead ? 0u : 0xffffu};
+    if (partial && !dead) {
+      lds_i32* ko = (lds_i32*)(lds + kVecOff + S * 1024 + 512);
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb) {
+        live[lb] = 0u;
+#pragma unroll 1
+        for (int i = 0; i < 16; ++i) {
+          const int kr = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
+          const int k_o = hperm ? ko[kr] : kb * kBT + kr;
+          if (pred_live_rolled(terms_s, a.pred.n_include, a.pred.n_exclude, q_o, k_o, a.pred.dense_bits,
+                               a.pred.dense_words))
+            live[lb] |= 1u << i;
+        }
+      }
+    }
+    auto scores = [&](int lb, f32x16& s, f32x16& dp) __attribute__((always_inline)) {
+      u32x4 ka[NKC], va[NKC];
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        ka[kc] = *(lds_u4*)(rd.row[kc] + SO + lb * 8192);
+        va[kc] = *(lds_u4*)(rd.row[kc] + SO + kTB + lb * 8192);
+      }
+      s = Mma<T>::mma(__builtin_bit_cast(Frag, ka[0]), qf[0], f32x16{0});
+      dp = Mma<T>::mma(__builtin_bit_cast(Frag, va[0]), df[0], f32x16{0});
+#pragma unroll
+      for (int kc = 1; kc < NKC; ++kc) {
+        s = Mma<T>::mma(__builtin_bit_cast(Frag, ka[kc]), qf[kc], s);
+        dp = Mma<T>::mma(__builtin_bit_cast(Frag, va[kc]), df[kc], dp);
+      }
+    };
+    auto grads = [&](int lb, const f32x16& s, const f32x16& dp, Frag* sf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        f32x8 sv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 8 * c + e;
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], a.c, nl2));
+          const float p = ((live[lb] >> i) & 1u) ? pe : 0.f;
+          sv[e] = p * (dp[i] - dr);
+        }
+        sf[c] = Mma<T>::cvt(sv);
+      }
+    };
+    auto accum = [&](int lb, const Frag* sf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int off = SO + (32 * lb + 16 * c) * 256;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) dqt[db] = Mma<T>::mma(tr_frag_sw<T>(rd, db, off), sf[c], dqt[db]);
+      }
+    };
+    f32x16 s0, dp0, s1, dp1;
+    Frag sf0[2], sf1[2];
+    scores(0, s0, dp0);
+    scores(1, s1, dp1);
+    grads(0, s0, dp0, sf0);
+    accum(0, sf0);
+    grads(1, s1, dp1, sf1);
+    accum(1, sf1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 12; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 12; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+#pragma unroll
+    for (int q_ = 0; q_ < 4; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 4; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+    }
+#pragma unroll
+    for (int q_ = 0; q_ < 4; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 4; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  };
+
+  const int nl = ((cint*)a.kv_num)[qb];
+  cint* klist = (cint*)(a.kv_idx + (int64_t)qb * a.pitch);
+  cbyte* plist = (cbyte*)(a.kv_partial + (int64_t)qb * a.pitch);
+  int kb_c = 0, kb_n = 0;
+  if (nl > 0) {
+    kb_c = klist[0];
+    dma(kb_c, 0);
+  }
+  if (nl > 1) kb_n = klist[1];
+  auto step = [&](auto SC, int t) __attribute__((always_inline)) {
+    constexpr int S = decltype(SC)::value;
+    const bool partial = plist[t] != 0;
+    dma_wait_all();
+    __syncthreads();
+    if (t + 1 < nl) dma(kb_n, S ^ 1);
+    const int kb = kb_c;
+    kb_c = kb_n;
+    if (t + 2 < nl) kb_n = klist[t + 2];
+    compute(SC, partial, kb);
+  };
+  int t = 0;
+  for (; t + 1 < nl; t += 2) {
+    step(std::integral_constant<int, 0>{}, t);
+    step(std::integral_constant<int, 1>{}, t + 1);
+  }
+  if (t < nl) step(std::integral_constant<int, 0>{}, t);
+
+  char* dqrow = a.dq + (bh * a.sb + (int64_t)row * a.sn) * ESZ;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int d0 = 32 * db + 8 * i4 + 4 * G;
+      f32x4 x = {dqt[db][4 * i4], dqt[db][4 * i4 + 1], dqt[db][4 * i4 + 2], dqt[db][4 * i4 + 3]};
+      x *= a.scale;
+      Mma<T>::store4(dqrow + d0 * ESZ, x);
+    }
+  }
+}
+
 // Transposed block lists: for key block kb, the query blocks whose list holds kb, in
 // ascending order, with the partial flag.  One thread per key block; each query block's
 // list is sorted, so membership is a binary search.  q_idx == nullptr: counts only.
@@ -378,10 +882,32 @@ int launch_bwd(const BwdK& k, int64_t BH, hipStream_t s) {
   const int64_t rows = BH * k.N;
   hipLaunchKernelGGL((bwd_pre_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, k, rows);
   PA_LAUNCH_CHECK("bwd_pre_kernel");
-  hipLaunchKernelGGL((bwd_dkdv_kernel<T, D>), dim3((unsigned)k.nb, (unsigned)BH), dim3(128), 0, s, k);
-  PA_LAUNCH_CHECK("bwd_dkdv_kernel");
-  hipLaunchKernelGGL((bwd_dq_kernel<T, D>), dim3((unsigned)k.nb, (unsigned)BH), dim3(128), 0, s, k);
-  PA_LAUNCH_CHECK("bwd_dq_kernel");
+  if constexpr (D == 128) {
+    // the dynamic LDS limit is raised once per device
+    static unsigned long long configured = 0ull;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev >= 64 || !((configured >> dev) & 1ull)) {
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_dkdv_stream_kernel<T>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kBwdSmem);
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_dq_stream_kernel<T>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kBwdSmem);
+      if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(bwd stream kernels)");
+      if (dev < 64) configured |= 1ull << dev;
+    }
+    const unsigned grid = (unsigned)(k.nb * BH);
+    hipLaunchKernelGGL(bwd_dkdv_stream_kernel<T>, dim3(grid), dim3(128), kBwdSmem, s, k);
+    PA_LAUNCH_CHECK("bwd_dkdv_stream_kernel");
+    hipLaunchKernelGGL(bwd_dq_stream_kernel<T>, dim3(grid), dim3(128), kBwdSmem, s, k);
+    PA_LAUNCH_CHECK("bwd_dq_stream_kernel");
+  } else {
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D>), dim3((unsigned)k.nb, (unsigned)BH), dim3(128), 0, s, k);
+    PA_LAUNCH_CHECK("bwd_dkdv_kernel");
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D>), dim3((unsigned)k.nb, (unsigned)BH), dim3(128), 0, s, k);
+    PA_LAUNCH_CHECK("bwd_dq_kernel");
+  }
   return PA_OK;
 }
 
@@ -413,8 +939,10 @@ extern "C" int pa_attn_bwd(const pa_attn_bwd_args* x, void* stream) {
   PA_CHECK_ARG(x->kv_num && x->q_num && (x->pitch == 0 || (x->kv_idx && x->kv_partial)) &&
                    (x->tpitch == 0 || (x->q_idx && x->q_partial)),
                "pa_attn_bwd: null index array");
-  PA_CHECK_ARG(x->sn >= x->D && x->sb >= x->sn, "pa_attn_bwd: strides sb=%lld sn=%lld", (long long)x->sb,
-               (long long)x->sn);
+  PA_CHECK_ARG(x->sn >= x->D && x->sb >= x->sn && x->sn < (1ll << 28), "pa_attn_bwd: strides sb=%lld sn=%lld",
+               (long long)x->sb, (long long)x->sn);
+  PA_CHECK_ARG((x->N / 64) * x->BH < (1ll << 31), "pa_attn_bwd: %lld blocks x %lld heads exceed one launch",
+               (long long)(x->N / 64), (long long)x->BH);
   auto al = [&](const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; };
   PA_CHECK_ARG(al(x->q) && al(x->k) && al(x->v) && al(x->o) && al(x->dout) && al(x->dq) && al(x->dk) && al(x->dv) &&
                    (x->sn * 2) % 16 == 0 && (x->sb * 2) % 16 == 0,

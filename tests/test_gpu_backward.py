@@ -72,10 +72,11 @@ def test_forward_then_backward(gpu):
     _check(grads, want, torch.bfloat16, "forward + backward")
 
 
-def test_permuted_basis_gives_the_permuted_gradients(gpu):
+@pytest.mark.parametrize("D", [64, 128])
+def test_permuted_basis_gives_the_permuted_gradients(gpu, D):
     """Tensors relabelled by rp8 with the mask evaluated through the permutation: the
     gradients are the identity-basis gradients relabelled."""
-    BH, N, D, name = 2, 1024, 64, "dilated-8"
+    BH, N, name = 2, 1024, "dilated-8"
     q, k, v = make_qkv(BH, N, D, torch.float16, seed=5)
     do = make_qkv(BH, N, D, torch.float16, seed=6)[0]
     p = op.residue_perm(N, 8)
