@@ -281,7 +281,14 @@ int pa_decode_fwd(const pa_decode_args* args, void* stream);
  * pa_index_transpose: for each of the nk key blocks, the query blocks whose list
  * (kv_idx / kv_num / kv_partial of an index built at BQ = A, pitch columns) holds it, in
  * ascending order, with the partial flag: q_num [nk], q_idx / q_partial [nk, tpitch].
+ * With kv_bits_off (pa_index_bits of the same index; may be NULL) also q_bits_off
+ * [nk, tpitch]: the word offset of the tile's bitmap, -1 for a full tile.
  * With q_idx NULL only q_num is written (size tpitch as max q_num, then call again).
+ *
+ * pa_index_bits_transpose: for every listed tile with kv_bits_off >= 0 (an index built
+ * at BQ = A = 64), its bitmap transposed into q_bits at the same word offset: bit c of
+ * word w of column k = pair (row 32 w + c, column k) of the tile is live.  q_bits has
+ * the size of kv_bits.
  *
  * pa_attn_bwd: gradients of o = softmax(scale q k^T masked) v for f16 / bf16, D = 64
  * or 128, N a multiple of 64, from the forward's lse (natural log, [BH, N], row stride
@@ -289,10 +296,16 @@ int pa_decode_fwd(const pa_decode_args* args, void* stream);
  * [BH, N, D] with the same element strides sb / sn.  The index is the forward's at
  * BQ = A = 64 and its transpose; the mask is evaluated on partial tiles only, at
  * (perm_q[r], perm_kv[c]) when the tables are given (tensors stay in index space).
- * dvec is a caller-owned fp32 [BH, N] workspace (rowsum(dO * O), same stride as lse). */
-int pa_index_transpose(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial, int32_t nq,
-                       int64_t pitch, int32_t nk, int32_t* q_num, int32_t* q_idx, int8_t* q_partial,
-                       int64_t tpitch, void* stream);
+ * dvec is a caller-owned fp32 [BH, N] workspace (rowsum(dO * O), same stride as lse).
+ * kv_bits_off / kv_bits (pa_index_bits) with q_bits_off / q_bits (their transpose) are
+ * all NULL or all given; given, the D = 128 kernels mask partial tiles from them instead
+ * of evaluating the mask. */
+int pa_index_transpose(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
+                       const int32_t* kv_bits_off, int32_t nq, int64_t pitch, int32_t nk, int32_t* q_num,
+                       int32_t* q_idx, int8_t* q_partial, int32_t* q_bits_off, int64_t tpitch, void* stream);
+
+int pa_index_bits_transpose(const int32_t* kv_bits_off, int32_t nq, int64_t pitch, const uint32_t* kv_bits,
+                            uint32_t* q_bits, void* stream);
 
 typedef struct pa_attn_bwd_args {
   const void* q;
@@ -318,6 +331,10 @@ typedef struct pa_attn_bwd_args {
   const int32_t* q_num;
   const int8_t* q_partial;
   int64_t tpitch;
+  const int32_t* kv_bits_off;
+  const uint32_t* kv_bits;
+  const int32_t* q_bits_off;
+  const uint32_t* q_bits;
   pa_mask mask;
 } pa_attn_bwd_args;
 

@@ -18,34 +18,54 @@ from .spec import DeviceMask, device_mask
 TILE = 64
 
 
-def transpose_index(kv_idx, kv_num, kv_partial, n_kv_blocks):
+def transpose_index(kv_idx, kv_num, kv_partial, n_kv_blocks, kv_bits_off=None):
     """Per key block, the query blocks whose list holds it (ascending) and the partial
-    flags: (q_idx int32 [nk, tpitch], q_num int32 [nk], q_partial int8 [nk, tpitch])."""
+    flags: (q_idx int32 [nk, tpitch], q_num int32 [nk], q_partial int8 [nk, tpitch],
+    q_bits_off int32 [nk, tpitch] or None).  With kv_bits_off (pa_index_bits of the same
+    index), q_bits_off holds each tile's bitmap offset (-1 for a full tile)."""
     _lib.require_device(kv_idx, kv_num, kv_partial)
     dev = kv_num.device
     nq, pitch = kv_idx.shape
     q_num = torch.empty(n_kv_blocks, dtype=torch.int32, device=dev)
     L = _lib.lib()
+    bo = _lib.ptr(kv_bits_off) if kv_bits_off is not None else None
     with torch.cuda.device(dev):
         st = _lib.stream_of(q_num)
-        _lib.check(L.pa_index_transpose(_lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial), nq, pitch,
-                                        n_kv_blocks, _lib.ptr(q_num), None, None, 0, st), "pa_index_transpose")
+        _lib.check(L.pa_index_transpose(_lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial), bo, nq, pitch,
+                                        n_kv_blocks, _lib.ptr(q_num), None, None, None, 0, st), "pa_index_transpose")
         tp = int(q_num.max().item()) if n_kv_blocks else 0
         q_idx = torch.zeros((n_kv_blocks, max(tp, 1)), dtype=torch.int32, device=dev)
         q_partial = torch.zeros((n_kv_blocks, max(tp, 1)), dtype=torch.int8, device=dev)
+        q_bits_off = torch.full((n_kv_blocks, max(tp, 1)), -1, dtype=torch.int32, device=dev) if bo else None
         if tp:
-            _lib.check(L.pa_index_transpose(_lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial), nq, pitch,
+            _lib.check(L.pa_index_transpose(_lib.ptr(kv_idx), _lib.ptr(kv_num), _lib.ptr(kv_partial), bo, nq, pitch,
                                             n_kv_blocks, _lib.ptr(q_num), _lib.ptr(q_idx), _lib.ptr(q_partial),
-                                            q_idx.shape[1], st), "pa_index_transpose")
-    return q_idx, q_num, q_partial
+                                            _lib.ptr(q_bits_off) if bo else None, q_idx.shape[1], st),
+                       "pa_index_transpose")
+    return q_idx, q_num, q_partial, q_bits_off
+
+
+def transpose_bits(kv_bits_off, kv_bits):
+    """The partial tiles' bitmaps (pa_index_bits at 64 x 64, row-major) transposed to
+    column-major at the same offsets."""
+    _lib.require_device(kv_bits_off, kv_bits)
+    q_bits = torch.zeros_like(kv_bits)
+    nq, pitch = kv_bits_off.shape
+    with torch.cuda.device(kv_bits.device):
+        _lib.check(_lib.lib().pa_index_bits_transpose(_lib.ptr(kv_bits_off), nq, pitch, _lib.ptr(kv_bits),
+                                                       _lib.ptr(q_bits), _lib.stream_of(q_bits)),
+                   "pa_index_bits_transpose")
+    return q_bits
 
 
 class BackwardPlan:
     """The 64 x 64 block index of `mask` at length N (and its transpose), built once.
     perm / perm_kv: index-space position -> original position, when the tensors given to
-    ``backward`` are relabelled (the mask is evaluated in original coordinates)."""
+    ``backward`` are relabelled (the mask is evaluated in original coordinates).
+    bitmaps=False leaves out the partial tiles' element bitmaps: the kernels then
+    evaluate the mask on partial tiles."""
 
-    def __init__(self, mask, N, device=None, perm=None, perm_kv=None):
+    def __init__(self, mask, N, device=None, perm=None, perm_kv=None, bitmaps=True):
         if N % TILE:
             raise ValueError(f"N={N} must be a multiple of {TILE}")
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
@@ -53,9 +73,15 @@ class BackwardPlan:
         if isinstance(mask, DeviceMask):
             raise ValueError("BackwardPlan takes a mask object (with perm / perm_kv), not a DeviceMask")
         self.dmask = device_mask(mask, N, dev, perm=perm, perm_kv=perm_kv)
-        kv_idx, kv_num, kv_partial = build_device(mask, N, TILE, TILE, perm=perm, perm_kv=perm_kv, device=dev)[:3]
+        built = build_device(mask, N, TILE, TILE, perm=perm, perm_kv=perm_kv, device=dev, bits=bitmaps)
+        kv_idx, kv_num, kv_partial = built[:3]
         self.kv_idx, self.kv_num, self.kv_partial = kv_idx.contiguous(), kv_num.contiguous(), kv_partial.contiguous()
-        self.q_idx, self.q_num, self.q_partial = transpose_index(self.kv_idx, self.kv_num, self.kv_partial, N // TILE)
+        # element bitmaps of the partial tiles, row-major for the dQ pass and transposed for
+        # the dK / dV pass, so neither evaluates the mask
+        self.kv_bits_off, self.kv_bits = (t.contiguous() for t in built[6]) if bitmaps else (None, None)
+        self.q_idx, self.q_num, self.q_partial, self.q_bits_off = transpose_index(
+            self.kv_idx, self.kv_num, self.kv_partial, N // TILE, self.kv_bits_off)
+        self.q_bits = transpose_bits(self.kv_bits_off, self.kv_bits) if bitmaps else None
 
     def backward(self, q, k, v, o, lse, do, scale=None, dq=None, dk=None, dv=None):
         """(dq, dk, dv) for [BH, N, D] f16 / bf16 tensors sharing strides; lse float32 [BH, N]
@@ -90,6 +116,9 @@ class BackwardPlan:
         a.pitch = self.kv_idx.shape[1]
         a.q_idx, a.q_num, a.q_partial = _lib.ptr(self.q_idx), _lib.ptr(self.q_num), _lib.ptr(self.q_partial)
         a.tpitch = self.q_idx.shape[1]
+        if self.kv_bits is not None:
+            a.kv_bits_off, a.kv_bits = _lib.ptr(self.kv_bits_off), _lib.ptr(self.kv_bits)
+            a.q_bits_off, a.q_bits = _lib.ptr(self.q_bits_off), _lib.ptr(self.q_bits)
         a.mask = self.dmask.struct()
         with torch.cuda.device(q.device):
             _lib.check(_lib.lib().pa_attn_bwd(ctypes.byref(a), _lib.stream_of(q)), "pa_attn_bwd")

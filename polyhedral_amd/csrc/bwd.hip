@@ -54,6 +54,10 @@ struct BwdK {
   const int32_t* q_num;
   const int8_t* q_partial;
   int64_t tpitch;
+  const int32_t* kv_bits_off;  // [nb, pitch] bitmap word offsets (-1: full), or NULL
+  const uint32_t* kv_bits;     // 64 rows x 2 words per partial tile, row-major
+  const int32_t* q_bits_off;   // [nb, tpitch], same offsets in the transposed lists
+  const uint32_t* q_bits;      // the same bitmaps transposed (64 columns x 2 words)
   Pred pred;
 };
 
@@ -353,20 +357,30 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void b
 // tile is read: unit u of row r sits at u ^ bswz(r), bswz(r) = 4 (r % 4) + (r / 4) % 4.
 // The 16 rows of a 16-byte row read land on 16 different units of the 256-byte bank
 // window, and the 4 rows of a transposed read on 4 different 64-byte groups.
-// LDS: two stages of two tiles, then per stage 1 KB of row vectors (lse, rowsum(dO O),
-// original row numbers), then the mask terms.
+// LDS: two stages of two tiles, then per stage 2 KB of row vectors (lse, rowsum(dO O),
+// original row numbers; the partial tile's bitmap at +1 KB), then the mask terms.
 constexpr int kTB = kBT * 256;
 constexpr int kStage = 2 * kTB;
 constexpr int kVecOff = 2 * kStage;
-constexpr int kTermsOff = kVecOff + 2 * 1024;
+constexpr int kVec = 2048;
+constexpr int kBitsAt = 1024;
+constexpr int kTermsOff = kVecOff + 2 * kVec;
 constexpr int kBwdSmem = kTermsOff + PA_MAX_TERMS * (int)sizeof(pa_term);
 
 typedef const __attribute__((address_space(3))) f32x4 lds_f4;
 typedef const __attribute__((address_space(3))) int32_t lds_i32;
+typedef const __attribute__((address_space(3))) u32x2 lds_u2;
 typedef const __attribute__((address_space(4))) int32_t cint;
 typedef const __attribute__((address_space(4))) int8_t cbyte;
 
 __device__ __forceinline__ int bswz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+
+// Live bits of a score block's 16 elements (element i = row or column 8 (i / 4) + 4 G +
+// i % 4 of the 32 the bitmap word covers).
+__device__ __forceinline__ uint32_t live16(uint32_t word, int G) {
+  const uint32_t x = word >> (4 * G);
+  return (x & 0xfu) | ((x >> 4) & 0xf0u) | ((x >> 8) & 0xf00u) | ((x >> 12) & 0xf000u);
+}
 
 // Per-lane LDS geometry of a staged tile (offsets of stage, tile, block and chunk are
 // immediates on top of these).
@@ -454,17 +468,21 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     dvoff[j] = (uint32_t)((lane >> 4) * rowb) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
-  // query block qb into stage S: Q and dO tiles; lse (and the original row numbers) by
-  // wave 0, rowsum(dO O) by wave 1
-  auto dma = [&](int qb, int S) __attribute__((always_inline)) {
+  const bool use_bits = a.q_bits != nullptr;
+  // query block qb into stage S: Q and dO tiles; lse (and, without bitmaps, the original
+  // row numbers) by wave 0, rowsum(dO O) by wave 1; a partial tile's bitmap (bo >= 0),
+  // columns 32 w .. 32 w + 31 by wave w
+  auto dma = [&](int qb, int bo, int S) __attribute__((always_inline)) {
     dma_tile_pair(lds0 + S * kStage, hq, hdo, rowb, (int64_t)qb * kBT, w, dvoff);
-    const uint32_t mv = lds0 + kVecOff + S * 1024;
+    const uint32_t mv = lds0 + kVecOff + S * kVec;
     if (w == 0) {
       dma_x1(mv, hlse + (int64_t)qb * 256, 4u * lane);
-      if (hperm) dma_x1(mv + 512, hperm + (int64_t)qb * 256, 4u * lane);
+      if (hperm && !use_bits) dma_x1(mv + 512, hperm + (int64_t)qb * 256, 4u * lane);
     } else {
       dma_x1(mv + 256, hdvec + (int64_t)qb * 256, 4u * lane);
     }
+    if (use_bits && bo >= 0)
+      dma_x1(mv + kBitsAt + 256 * w, reinterpret_cast<const char*>(a.q_bits + bo) + 256 * w, 4u * lane);
   };
 
   const TileReads rd = tile_reads(lds, lane);
@@ -488,8 +506,14 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int S = decltype(SC)::value;
     constexpr int SO = S * kStage;
     uint32_t live[2] = {0xffffu, 0xffffu};
-    if (partial) {
-      lds_i32* qo = (lds_i32*)(lds + kVecOff + S * 1024 + 512);
+    if (partial && use_bits) {
+      // this lane's column of the tile: rows 0..31, 32..63
+      const u32x2 bw = *(lds_u2*)(lds + kVecOff + S * kVec + kBitsAt + (32 * w + m) * 8);
+      const uint32_t b0 = bw.x, b1 = bw.y;
+      live[0] = live16(b0, G);
+      live[1] = live16(b1, G);
+    } else if (partial) {
+      lds_i32* qo = (lds_i32*)(lds + kVecOff + S * kVec + 512);
 #pragma unroll
       for (int lb = 0; lb < 2; ++lb) {
         live[lb] = 0u;
@@ -524,8 +548,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       f32x4 l4[4], d4[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        l4[j] = *(lds_f4*)(vrow + S * 1024 + (32 * lb + 8 * j) * 4);
-        d4[j] = *(lds_f4*)(vrow + S * 1024 + 256 + (32 * lb + 8 * j) * 4);
+        l4[j] = *(lds_f4*)(vrow + S * kVec + (32 * lb + 8 * j) * 4);
+        d4[j] = *(lds_f4*)(vrow + S * kVec + 256 + (32 * lb + 8 * j) * 4);
       }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -610,21 +634,28 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int nl = ((cint*)a.q_num)[kb];
   cint* qlist = (cint*)(a.q_idx + (int64_t)kb * a.tpitch);
   cbyte* plist = (cbyte*)(a.q_partial + (int64_t)kb * a.tpitch);
-  int qb_c = 0, qb_n = 0;
+  cint* olist = (cint*)(use_bits ? a.q_bits_off + (int64_t)kb * a.tpitch : a.q_idx);
+  // listed tile t: query block and bitmap offset (-1: full; without bitmaps 0 = partial)
+  auto tile_of = [&](int t, int& qb, int& bo) __attribute__((always_inline)) {
+    qb = qlist[t];
+    bo = use_bits ? olist[t] : (plist[t] != 0 ? 0 : -1);
+  };
+  int qb_c = 0, bo_c = -1, qb_n = 0, bo_n = -1;
   if (nl > 0) {
-    qb_c = qlist[0];
-    dma(qb_c, 0);
+    tile_of(0, qb_c, bo_c);
+    dma(qb_c, bo_c, 0);
   }
-  if (nl > 1) qb_n = qlist[1];
+  if (nl > 1) tile_of(1, qb_n, bo_n);
   auto step = [&](auto SC, int t) __attribute__((always_inline)) {
     constexpr int S = decltype(SC)::value;
-    const bool partial = plist[t] != 0;
     dma_wait_all();
     __syncthreads();  // stage S is in; every wave is past its reads of stage S ^ 1
-    if (t + 1 < nl) dma(qb_n, S ^ 1);
+    if (t + 1 < nl) dma(qb_n, bo_n, S ^ 1);
     const int qb = qb_c;
+    const bool partial = bo_c >= 0;
     qb_c = qb_n;
-    if (t + 2 < nl) qb_n = qlist[t + 2];
+    bo_c = bo_n;
+    if (t + 2 < nl) tile_of(t + 2, qb_n, bo_n);
     compute(SC, partial, qb);
   };
   int t = 0;
@@ -679,10 +710,15 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     dvoff[j] = (uint32_t)((lane >> 4) * rowb) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
-  // key block kb into stage S: K and V tiles; the original key numbers by wave 0
-  auto dma = [&](int kb, int S) __attribute__((always_inline)) {
+  const bool use_bits = a.kv_bits != nullptr;
+  // key block kb into stage S: K and V tiles; without bitmaps the original key numbers by
+  // wave 0; a partial tile's bitmap (bo >= 0), rows 32 w .. 32 w + 31 by wave w
+  auto dma = [&](int kb, int bo, int S) __attribute__((always_inline)) {
     dma_tile_pair(lds0 + S * kStage, hk, hv, rowb, (int64_t)kb * kBT, w, dvoff);
-    if (hperm && w == 0) dma_x1(lds0 + kVecOff + S * 1024 + 512, hperm + (int64_t)kb * 256, 4u * lane);
+    const uint32_t mv = lds0 + kVecOff + S * kVec;
+    if (hperm && !use_bits && w == 0) dma_x1(mv + 512, hperm + (int64_t)kb * 256, 4u * lane);
+    if (use_bits && bo >= 0)
+      dma_x1(mv + kBitsAt + 256 * w, reinterpret_cast<const char*>(a.kv_bits + bo) + 256 * w, 4u * lane);
   };
 
   const TileReads rd = tile_reads(lds, lane);
@@ -706,8 +742,14 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int S = decltype(SC)::value;
     constexpr int SO = S * kStage;
     uint32_t live[2] = {dead ? 0u : 0xffffu, dead ? 0u : 0xffffu};
-    if (partial && !dead) {
-      lds_i32* ko = (lds_i32*)(lds + kVecOff + S * 1024 + 512);
+    if (partial && !dead && use_bits) {
+      // this lane's row of the tile: columns 0..31, 32..63
+      const u32x2 bw = *(lds_u2*)(lds + kVecOff + S * kVec + kBitsAt + (32 * w + m) * 8);
+      const uint32_t b0 = bw.x, b1 = bw.y;
+      live[0] = live16(b0, G);
+      live[1] = live16(b1, G);
+    } else if (partial && !dead) {
+      lds_i32* ko = (lds_i32*)(lds + kVecOff + S * kVec + 512);
 #pragma unroll
       for (int lb = 0; lb < 2; ++lb) {
         live[lb] = 0u;
@@ -809,21 +851,27 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int nl = ((cint*)a.kv_num)[qb];
   cint* klist = (cint*)(a.kv_idx + (int64_t)qb * a.pitch);
   cbyte* plist = (cbyte*)(a.kv_partial + (int64_t)qb * a.pitch);
-  int kb_c = 0, kb_n = 0;
+  cint* olist = (cint*)(use_bits ? a.kv_bits_off + (int64_t)qb * a.pitch : a.kv_idx);
+  auto tile_of = [&](int t, int& kb, int& bo) __attribute__((always_inline)) {
+    kb = klist[t];
+    bo = use_bits ? olist[t] : (plist[t] != 0 ? 0 : -1);
+  };
+  int kb_c = 0, bo_c = -1, kb_n = 0, bo_n = -1;
   if (nl > 0) {
-    kb_c = klist[0];
-    dma(kb_c, 0);
+    tile_of(0, kb_c, bo_c);
+    dma(kb_c, bo_c, 0);
   }
-  if (nl > 1) kb_n = klist[1];
+  if (nl > 1) tile_of(1, kb_n, bo_n);
   auto step = [&](auto SC, int t) __attribute__((always_inline)) {
     constexpr int S = decltype(SC)::value;
-    const bool partial = plist[t] != 0;
     dma_wait_all();
     __syncthreads();
-    if (t + 1 < nl) dma(kb_n, S ^ 1);
+    if (t + 1 < nl) dma(kb_n, bo_n, S ^ 1);
     const int kb = kb_c;
+    const bool partial = bo_c >= 0;
     kb_c = kb_n;
-    if (t + 2 < nl) kb_n = klist[t + 2];
+    bo_c = bo_n;
+    if (t + 2 < nl) tile_of(t + 2, kb_n, bo_n);
     compute(SC, partial, kb);
   };
   int t = 0;
@@ -850,8 +898,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // ascending order, with the partial flag.  One thread per key block; each query block's
 // list is sorted, so membership is a binary search.  q_idx == nullptr: counts only.
 __global__ __launch_bounds__(256) void transpose_kernel(const int32_t* kv_idx, const int32_t* kv_num,
-                                                        const int8_t* kv_partial, int32_t nq, int64_t pitch,
-                                                        int32_t nk, int32_t* q_num, int32_t* q_idx, int8_t* q_partial,
+                                                        const int8_t* kv_partial, const int32_t* kv_bits_off,
+                                                        int32_t nq, int64_t pitch, int32_t nk, int32_t* q_num,
+                                                        int32_t* q_idx, int8_t* q_partial, int32_t* q_bits_off,
                                                         int64_t tp) {
   const int kb = blockIdx.x * 256 + threadIdx.x;
   if (kb >= nk) return;
@@ -870,11 +919,26 @@ __global__ __launch_bounds__(256) void transpose_kernel(const int32_t* kv_idx, c
       if (q_idx && n < tp) {
         q_idx[(int64_t)kb * tp + n] = qb;
         q_partial[(int64_t)kb * tp + n] = kv_partial[(int64_t)qb * pitch + lo];
+        if (q_bits_off) q_bits_off[(int64_t)kb * tp + n] = kv_bits_off[(int64_t)qb * pitch + lo];
       }
       ++n;
     }
   }
   q_num[kb] = n;
+}
+
+// One 64 x 64 bitmap per work-group of 64 threads (listed tile j of query block i, when
+// kv_bits_off[i, j] >= 0): thread k assembles column k from the 64 row words.
+__global__ __launch_bounds__(64) void bits_transpose_kernel(const int32_t* kv_bits_off, int64_t pitch,
+                                                             const uint32_t* kv_bits, uint32_t* q_bits) {
+  const int64_t off = kv_bits_off[(int64_t)blockIdx.y * pitch + blockIdx.x];
+  if (off < 0) return;
+  const int k = threadIdx.x;
+  uint32_t col[2] = {0u, 0u};
+#pragma unroll 8
+  for (int r = 0; r < 64; ++r) col[r >> 5] |= ((kv_bits[off + 2 * r + (k >> 5)] >> (k & 31)) & 1u) << (r & 31);
+  q_bits[off + 2 * k] = col[0];
+  q_bits[off + 2 * k + 1] = col[1];
 }
 
 template <typename T, int D>
@@ -914,16 +978,31 @@ int launch_bwd(const BwdK& k, int64_t BH, hipStream_t s) {
 }  // namespace
 }  // namespace pa
 
-extern "C" int pa_index_transpose(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial, int32_t nq,
-                                  int64_t pitch, int32_t nk, int32_t* q_num, int32_t* q_idx, int8_t* q_partial,
-                                  int64_t tpitch, void* stream) {
+extern "C" int pa_index_transpose(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
+                                  const int32_t* kv_bits_off, int32_t nq, int64_t pitch, int32_t nk, int32_t* q_num,
+                                  int32_t* q_idx, int8_t* q_partial, int32_t* q_bits_off, int64_t tpitch,
+                                  void* stream) {
   PA_CHECK_ARG(kv_num && q_num && nq >= 1 && nk >= 1 && pitch >= 0 && tpitch >= 0, "pa_index_transpose: bad arguments");
-  PA_CHECK_ARG(pitch == 0 || kv_idx, "pa_index_transpose: null kv_idx");
+  PA_CHECK_ARG(pitch == 0 || (kv_idx && kv_partial), "pa_index_transpose: null kv_idx / kv_partial");
   PA_CHECK_ARG(!q_idx || q_partial, "pa_index_transpose: q_idx needs q_partial");
+  PA_CHECK_ARG(!q_bits_off || (kv_bits_off && q_idx), "pa_index_transpose: q_bits_off needs kv_bits_off and q_idx");
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(pa::transpose_kernel, dim3((unsigned)((nk + 255) / 256)), dim3(256), 0, s, kv_idx, kv_num,
-                     kv_partial, nq, pitch, nk, q_num, q_idx, q_partial, tpitch);
+                     kv_partial, kv_bits_off, nq, pitch, nk, q_num, q_idx, q_partial, q_bits_off, tpitch);
   PA_LAUNCH_CHECK("transpose_kernel");
+  return PA_OK;
+}
+
+extern "C" int pa_index_bits_transpose(const int32_t* kv_bits_off, int32_t nq, int64_t pitch, const uint32_t* kv_bits,
+                                       uint32_t* q_bits, void* stream) {
+  PA_CHECK_ARG(nq >= 1 && nq <= 65535 && pitch >= 0 && pitch < (1ll << 31), "pa_index_bits_transpose: nq=%d pitch=%lld",
+               nq, (long long)pitch);
+  if (pitch == 0) return PA_OK;
+  PA_CHECK_ARG(kv_bits_off && kv_bits && q_bits, "pa_index_bits_transpose: null array");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(pa::bits_transpose_kernel, dim3((unsigned)pitch, (unsigned)nq), dim3(64), 0, s, kv_bits_off,
+                     pitch, kv_bits, q_bits);
+  PA_LAUNCH_CHECK("bits_transpose_kernel");
   return PA_OK;
 }
 
@@ -975,6 +1054,12 @@ extern "C" int pa_attn_bwd(const pa_attn_bwd_args* x, void* stream) {
   k.q_num = x->q_num;
   k.q_partial = x->q_partial;
   k.tpitch = x->tpitch;
+  const bool nb_ = !x->kv_bits_off, nk_ = !x->kv_bits, qo_ = !x->q_bits_off, qk_ = !x->q_bits;
+  PA_CHECK_ARG(nb_ == nk_ && nb_ == qo_ && nb_ == qk_, "pa_attn_bwd: the four bitmap arrays are all NULL or all given");
+  k.kv_bits_off = x->kv_bits_off;
+  k.kv_bits = x->kv_bits;
+  k.q_bits_off = x->q_bits_off;
+  k.q_bits = x->q_bits;
   k.pred = pa::make_pred(x->mask);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (x->dtype == PA_BF16) return x->D == 128 ? pa::launch_bwd<__bf16, 128>(k, x->BH, s) : pa::launch_bwd<__bf16, 64>(k, x->BH, s);

@@ -44,16 +44,26 @@ def _check(grads, want, dtype, what):
 @pytest.mark.parametrize("name", ["causal", "window-128", "dilated-8", "band256+lat16", "sinks4+win256",
                                   "local256+str8", "prefixlm-2048"])
 def test_gradients_equal_oracle(gpu, name, dtype, D):
+    _gradients_case(gpu, name, dtype, D, True)
+
+
+@pytest.mark.parametrize("name", ["causal", "band256+lat16", "sinks4+win256", "prefixlm-2048"])
+def test_gradients_without_bitmaps(gpu, name):
+    """Partial tiles masked by evaluating the mask (no element bitmaps given)."""
+    _gradients_case(gpu, name, torch.bfloat16, 128, False)
+
+
+def _gradients_case(gpu, name, dtype, D, bitmaps):
     BH, N = 2, 1024
     q, k, v = make_qkv(BH, N, D, dtype, seed=D)
     do = make_qkv(BH, N, D, dtype, seed=D + 1)[0]
     rows = oatt.spec_rows(om.NAMED[name], N)
     o, lse, want = _oracle(q, k, v, do, rows)
-    plan = pbwd.BackwardPlan(numpy_mask(name), N, gpu)
+    plan = pbwd.BackwardPlan(numpy_mask(name), N, gpu, bitmaps=bitmaps)
     dev = lambda x: x.to(gpu)
     grads = plan.backward(dev(q), dev(k), dev(v), torch.from_numpy(o).to(dtype).to(gpu),
                           torch.from_numpy(lse).float().to(gpu), dev(do))
-    _check(grads, want, dtype, f"{name} {dtype} D={D}")
+    _check(grads, want, dtype, f"{name} {dtype} D={D} bitmaps={bitmaps}")
 
 
 def test_forward_then_backward(gpu):
@@ -116,3 +126,21 @@ def test_dead_rows_and_transposed_index(gpu):
         assert q_num[kb] == len(holders)
         assert [int(x) for x in q_idx[kb, :q_num[kb]]] == [h[0] for h in holders]
         assert [int(x) for x in q_part[kb, :q_num[kb]]] == [int(h[1]) for h in holders]
+    # bitmaps: a tile's offset is the same in both lists, its transposed bitmap is the
+    # row-major one transposed, and its bits are the dense mask's
+    kv_off, q_off = plan.kv_bits_off.cpu().numpy(), plan.q_bits_off.cpu().numpy()
+    rb, cb = (t.cpu().numpy().view(np.uint32) for t in (plan.kv_bits, plan.q_bits))
+    n_partial = 0
+    for qb in range(nb):
+        for j in range(kv_num[qb]):
+            kb, off = int(kv_idx[qb, j]), int(kv_off[qb, j])
+            assert (off >= 0) == bool(kv_part[qb, j])
+            assert q_off[kb, list(q_idx[kb, :q_num[kb]]).index(qb)] == off
+            if off < 0:
+                continue
+            n_partial += 1
+            rows = np.unpackbits(rb[off:off + 128].view(np.uint8), bitorder="little").reshape(64, 64)
+            cols = np.unpackbits(cb[off:off + 128].view(np.uint8), bitorder="little").reshape(64, 64)
+            assert np.array_equal(rows, M[qb * 64:qb * 64 + 64, kb * 64:kb * 64 + 64])
+            assert np.array_equal(cols.T, rows)
+    assert n_partial > 0
