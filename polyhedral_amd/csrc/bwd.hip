@@ -422,16 +422,19 @@ __device__ __forceinline__ typename Mma<T>::frag tr_frag_sw(const TileReads& t, 
 }
 
 // DMA of rows r0 .. r0 + 63 of two [N, 128] tensors (row pitch rowb bytes, heads already
-// applied) into stage tiles at LDS m0 and m0 + kTB.  Wave w moves rows 32 w .. 32 w + 31;
-// its instruction i writes rows 32 w + 4 i + l / 16, lane l unit l % 16, fetching the
-// unit the swizzle stores there: (l % 16) ^ (4 (l / 16) + i % 4) (dvoff[i % 4]).
-__device__ __forceinline__ void dma_tile_pair(uint32_t m0, const char* g0, const char* g1, int64_t rowb, int64_t r0,
-                                              int w, const uint32_t* dvoff) {
+// applied) into stage tiles at LDS m0 and m0 + kTB, in four parts (instructions 2 part,
+// 2 part + 1 of each tensor), so that a tile's DMA can be spread over the previous tile's
+// MFMAs.  Wave w moves rows 32 w .. 32 w + 31; its instruction i writes rows
+// 32 w + 4 i + l / 16, lane l unit l % 16, fetching the unit the swizzle stores there:
+// (l % 16) ^ (4 (l / 16) + i % 4) (dvoff[i % 4]).
+__device__ __forceinline__ void dma_tile_part(uint32_t m0, const char* g0, const char* g1, int64_t rowb, int64_t r0,
+                                              int w, const uint32_t* dvoff, int part) {
   const char* a0 = g0 + (r0 + 32 * w) * rowb;
   const char* a1 = g1 + (r0 + 32 * w) * rowb;
   const uint32_t mw = m0 + (uint32_t)(32 * w * 256);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int ii = 0; ii < 2; ++ii) {
+    const int i = 2 * part + ii;
     dma_x4(mw + i * 1024, a0 + 4 * i * rowb, dvoff[i & 3]);
     dma_x4(mw + kTB + i * 1024, a1 + 4 * i * rowb, dvoff[i & 3]);
   }
@@ -472,8 +475,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // query block qb into stage S: Q and dO tiles; lse (and, without bitmaps, the original
   // row numbers) by wave 0, rowsum(dO O) by wave 1; a partial tile's bitmap (bo >= 0),
   // columns 32 w .. 32 w + 31 by wave w
-  auto dma = [&](int qb, int bo, int S) __attribute__((always_inline)) {
-    dma_tile_pair(lds0 + S * kStage, hq, hdo, rowb, (int64_t)qb * kBT, w, dvoff);
+  auto dma = [&](int qb, int bo, int S, int part) __attribute__((always_inline)) {
+    dma_tile_part(lds0 + S * kStage, hq, hdo, rowb, (int64_t)qb * kBT, w, dvoff, part);
+    if (part) return;
     const uint32_t mv = lds0 + kVecOff + S * kVec;
     if (w == 0) {
       dma_x1(mv, hlse + (int64_t)qb * 256, 4u * lane);
@@ -502,7 +506,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   //   C  dV^T += dO^T P, dK^T += Q^T dS of rows 0..31, beside the scores' gradient of 32..63;
   //   D  dV^T, dK^T of rows 32..63.
   // Element i of a score block is query row 32 lb + 8 (i / 4) + 4 G + i % 4, key `key`.
-  auto compute = [&](auto SC, bool partial, int qb) __attribute__((always_inline)) {
+  // pre(k) issues part k of the next tile's DMA (all four before the first MFMA: spread
+  // over the phases they were no faster).
+  auto compute = [&](auto SC, bool partial, int qb, auto&& pre) __attribute__((always_inline)) {
     constexpr int S = decltype(SC)::value;
     constexpr int SO = S * kStage;
     uint32_t live[2] = {0xffffu, 0xffffu};
@@ -543,14 +549,17 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         dp = Mma<T>::mma(__builtin_bit_cast(Frag, da[kc]), vf[kc], dp);
       }
     };
-    // P and dS of rows 32 lb .. +31 as MFMA operands (chunks of 16 rows)
-    auto grads = [&](int lb, const f32x16& s, const f32x16& dp, Frag* pf, Frag* sf) __attribute__((always_inline)) {
-      f32x4 l4[4], d4[4];
+    // lse and rowsum(dO O) of the lane's 16 rows of block lb
+    auto vec_reads = [&](int lb, f32x4* l4, f32x4* d4) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         l4[j] = *(lds_f4*)(vrow + S * kVec + (32 * lb + 8 * j) * 4);
         d4[j] = *(lds_f4*)(vrow + S * kVec + 256 + (32 * lb + 8 * j) * 4);
       }
+    };
+    // P and dS of rows 32 lb .. +31 as MFMA operands (chunks of 16 rows)
+    auto grads = [&](int lb, const f32x16& s, const f32x16& dp, const f32x4* l4, const f32x4* d4, Frag* pf,
+                     Frag* sf) __attribute__((always_inline)) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         f32x8 pv, sv;
@@ -567,35 +576,50 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         sf[c] = Mma<T>::cvt(sv);
       }
     };
-    // dV^T += dO^T P, dK^T += Q^T dS for rows 32 lb .. +31
-    auto accum = [&](int lb, const Frag* pf, const Frag* sf) __attribute__((always_inline)) {
+    // dV^T += dO^T P, dK^T += Q^T dS for rows 32 lb .. +31: the transposed fragments of dO
+    // and Q (chunk c, block db at 4 c + db) are read first, into registers
+    auto tr_reads = [&](int lb, Frag* fd, Frag* fq) __attribute__((always_inline)) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int off = SO + (32 * lb + 16 * c) * 256;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          dvt[db] = Mma<T>::mma(tr_frag_sw<T>(rd, db, off + kTB), pf[c], dvt[db]);
-          dkt[db] = Mma<T>::mma(tr_frag_sw<T>(rd, db, off), sf[c], dkt[db]);
+          fd[4 * c + db] = tr_frag_sw<T>(rd, db, off + kTB);
+          fq[4 * c + db] = tr_frag_sw<T>(rd, db, off);
         }
       }
     };
+    auto accum = [&](const Frag* fd, const Frag* fq, const Frag* pf, const Frag* sf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          dvt[db] = Mma<T>::mma(fd[4 * c + db], pf[c], dvt[db]);
+          dkt[db] = Mma<T>::mma(fq[4 * c + db], sf[c], dkt[db]);
+        }
+    };
     f32x16 s0, dp0, s1, dp1;
-    Frag pf0[2], sf0[2], pf1[2], sf1[2];
+    f32x4 l4a[4], d4a[4], l4b[4], d4b[4];
+    Frag pf0[2], sf0[2], pf1[2], sf1[2], fd[8], fq[8];
+    // A: the row vectors and 4 reads ahead, then one read per MFMA
+    pre(0);
+    pre(1);
+    pre(2);
+    pre(3);
+    vec_reads(0, l4a, d4a);
     scores(0, s0, dp0);
-    scores(1, s1, dp1);
-    grads(0, s0, dp0, pf0, sf0);
-    accum(0, pf0, sf0);
-    grads(1, s1, dp1, pf1, sf1);
-    accum(1, pf1, sf1);
-    // A: 4 reads ahead, then one read per MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
 #pragma unroll
     for (int q_ = 0; q_ < 12; ++q_) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_barrier(0);
     // B: rows 32..63's reads and MFMAs, rows 0..31's gradient in the VALU slots
+    vec_reads(1, l4b, d4b);
+    scores(1, s1, dp1);
+    grads(0, s0, dp0, l4a, d4a, pf0, sf0);
     __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
 #pragma unroll
     for (int q_ = 0; q_ < 12; ++q_) {
@@ -608,27 +632,24 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
     }
-    // C: rows 0..31's accumulation, rows 32..63's gradient in the VALU slots
-    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // C: all transposed reads of rows 0..31 first, then their MFMAs with rows 32..63's
+    // gradient in the VALU slots
+    tr_reads(0, fd, fq);
+    grads(1, s1, dp1, l4b, d4b, pf1, sf1);
+    accum(fd, fq, pf0, sf0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 32, 0);
 #pragma unroll
-    for (int q_ = 0; q_ < 12; ++q_) {
+    for (int q_ = 0; q_ < 16; ++q_) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
     }
-#pragma unroll
-    for (int q_ = 0; q_ < 4; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-    }
-    // D: rows 32..63's accumulation
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-    for (int q_ = 0; q_ < 12; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // D: rows 32..63
+    tr_reads(1, fd, fq);
+    accum(fd, fq, pf1, sf1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 32, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
   };
 
   const int nl = ((cint*)a.q_num)[kb];
@@ -643,20 +664,23 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   int qb_c = 0, bo_c = -1, qb_n = 0, bo_n = -1;
   if (nl > 0) {
     tile_of(0, qb_c, bo_c);
-    dma(qb_c, bo_c, 0);
+#pragma unroll
+    for (int part = 0; part < 4; ++part) dma(qb_c, bo_c, 0, part);
   }
   if (nl > 1) tile_of(1, qb_n, bo_n);
   auto step = [&](auto SC, int t) __attribute__((always_inline)) {
     constexpr int S = decltype(SC)::value;
     dma_wait_all();
     __syncthreads();  // stage S is in; every wave is past its reads of stage S ^ 1
-    if (t + 1 < nl) dma(qb_n, bo_n, S ^ 1);
-    const int qb = qb_c;
+    const bool more = t + 1 < nl;
+    const int qb = qb_c, qb_d = qb_n, bo_d = bo_n;
     const bool partial = bo_c >= 0;
     qb_c = qb_n;
     bo_c = bo_n;
     if (t + 2 < nl) tile_of(t + 2, qb_n, bo_n);
-    compute(SC, partial, qb);
+    compute(SC, partial, qb, [&](int part) __attribute__((always_inline)) {
+      if (more) dma(qb_d, bo_d, S ^ 1, part);
+    });
   };
   int t = 0;
   for (; t + 1 < nl; t += 2) {
@@ -713,8 +737,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const bool use_bits = a.kv_bits != nullptr;
   // key block kb into stage S: K and V tiles; without bitmaps the original key numbers by
   // wave 0; a partial tile's bitmap (bo >= 0), rows 32 w .. 32 w + 31 by wave w
-  auto dma = [&](int kb, int bo, int S) __attribute__((always_inline)) {
-    dma_tile_pair(lds0 + S * kStage, hk, hv, rowb, (int64_t)kb * kBT, w, dvoff);
+  auto dma = [&](int kb, int bo, int S, int part) __attribute__((always_inline)) {
+    dma_tile_part(lds0 + S * kStage, hk, hv, rowb, (int64_t)kb * kBT, w, dvoff, part);
+    if (part) return;
     const uint32_t mv = lds0 + kVecOff + S * kVec;
     if (hperm && !use_bits && w == 0) dma_x1(mv + 512, hperm + (int64_t)kb * 256, 4u * lane);
     if (use_bits && bo >= 0)
@@ -738,7 +763,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // keys 32..63 beside the gradient of keys 0..31; C dQ^T += K^T dS^T of keys 0..31 beside
   // the gradient of 32..63; D dQ^T of keys 32..63.  Element i of a score block is key
   // 32 lb + 8 (i / 4) + 4 G + i % 4, query `row`.
-  auto compute = [&](auto SC, bool partial, int kb) __attribute__((always_inline)) {
+  auto compute = [&](auto SC, bool partial, int kb, auto&& pre) __attribute__((always_inline)) {
     constexpr int S = decltype(SC)::value;
     constexpr int SO = S * kStage;
     uint32_t live[2] = {dead ? 0u : 0xffffu, dead ? 0u : 0xffffu};
@@ -792,60 +817,66 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         sf[c] = Mma<T>::cvt(sv);
       }
     };
-    auto accum = [&](int lb, const Frag* sf) __attribute__((always_inline)) {
+    // dQ^T += K^T dS^T for keys 32 lb .. +31: the transposed K fragments (chunk c, block db
+    // at 4 c + db) are read first, into registers
+    auto tr_reads = [&](int lb, Frag* fk) __attribute__((always_inline)) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int off = SO + (32 * lb + 16 * c) * 256;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) dqt[db] = Mma<T>::mma(tr_frag_sw<T>(rd, db, off), sf[c], dqt[db]);
+        for (int db = 0; db < NDB; ++db) fk[4 * c + db] = tr_frag_sw<T>(rd, db, off);
       }
     };
+    auto accum = [&](const Frag* fk, const Frag* sf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) dqt[db] = Mma<T>::mma(fk[4 * c + db], sf[c], dqt[db]);
+    };
     f32x16 s0, dp0, s1, dp1;
-    Frag sf0[2], sf1[2];
+    Frag sf0[2], sf1[2], fk[8];
+    pre(0);
+    pre(1);
+    pre(2);
+    pre(3);
     scores(0, s0, dp0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 12; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_barrier(0);
     scores(1, s1, dp1);
     grads(0, s0, dp0, sf0);
-    accum(0, sf0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q_ = 0; q_ < 12; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+#pragma unroll
+    for (int q_ = 0; q_ < 4; ++q_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    tr_reads(0, fk);
     grads(1, s1, dp1, sf1);
-    accum(1, sf1);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    accum(fk, sf0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
 #pragma unroll
-    for (int q_ = 0; q_ < 12; ++q_) {
+    for (int q_ = 0; q_ < 8; ++q_) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int q_ = 0; q_ < 12; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-    }
-#pragma unroll
-    for (int q_ = 0; q_ < 4; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-    for (int q_ = 0; q_ < 4; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-    }
-#pragma unroll
-    for (int q_ = 0; q_ < 4; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-    for (int q_ = 0; q_ < 4; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    tr_reads(1, fk);
+    accum(fk, sf1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   };
 
   const int nl = ((cint*)a.kv_num)[qb];
@@ -859,20 +890,23 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   int kb_c = 0, bo_c = -1, kb_n = 0, bo_n = -1;
   if (nl > 0) {
     tile_of(0, kb_c, bo_c);
-    dma(kb_c, bo_c, 0);
+#pragma unroll
+    for (int part = 0; part < 4; ++part) dma(kb_c, bo_c, 0, part);
   }
   if (nl > 1) tile_of(1, kb_n, bo_n);
   auto step = [&](auto SC, int t) __attribute__((always_inline)) {
     constexpr int S = decltype(SC)::value;
     dma_wait_all();
     __syncthreads();
-    if (t + 1 < nl) dma(kb_n, bo_n, S ^ 1);
-    const int kb = kb_c;
+    const bool more = t + 1 < nl;
+    const int kb = kb_c, kb_d = kb_n, bo_d = bo_n;
     const bool partial = bo_c >= 0;
     kb_c = kb_n;
     bo_c = bo_n;
     if (t + 2 < nl) tile_of(t + 2, kb_n, bo_n);
-    compute(SC, partial, kb);
+    compute(SC, partial, kb, [&](int part) __attribute__((always_inline)) {
+      if (more) dma(kb_d, bo_d, S ^ 1, part);
+    });
   };
   int t = 0;
   for (; t + 1 < nl; t += 2) {
