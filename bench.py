@@ -201,51 +201,56 @@ def measure_decode(wl, q, k, v, residues=(0, 16), reps=200, warmup=20):
                 "HIP graph replay; algorithmic bytes = live K/V rows + appended rows + q + o", **out)
 
 
-def measure_backward(wl, q, k, v, residue, reps=20, warmup=5):
-    """The backward of the workload's whole mask in one pass (pa_attn_bwd: pre-pass, dK/dV
-    and dQ kernels over 64 x 64 tiles) in the residue-`residue` basis (0: identity), the
-    tensors relabelled before the timed region.  Live FLOP = 8 D per live pair and head
-    (dV, dP, dQ, dK; the recomputed scores are not counted)."""
+def measure_backward(wl, q, k, v, o, lse, residue, reps=20, warmup=5):
+    """The backward of the workload's mask from the forward's o and lse (pa_attn_bwd over
+    64 x 64 tiles: pre-pass, dK/dV and dQ kernels), split into the forward's pieces, each
+    in its own basis (SplitBackward: the permuted pieces' tensors gathered and their
+    gradients scattered back inside the timed region).  For comparison, the whole mask in
+    one pass in the residue-`residue` basis, the tensors relabelled before the timed
+    region.  Live FLOP = 8 D per live pair and head (dV, dP, dQ, dK; the recomputed scores
+    are not counted)."""
     import torch
 
-    from polyhedral_amd import attention as pattn
     from polyhedral_amd import backward as pbwd
-    from polyhedral_amd import index as pindex
     from polyhedral_amd.perm import residue_perm
-    from polyhedral_amd.spec import device_mask
     H, L, D = wl.H, wl.L, wl.D
+    dop = torch.randn(q.shape, generator=torch.Generator().manual_seed(7)).to(q.dtype).to(q.device)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(reps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / reps
+
+    split = pbwd.SplitBackward(wl.pieces, L, q.device)
+    ms = timed(lambda: split.backward(q, k, v, o, lse, dop))
+    tiles = split.tiles
+    # the whole mask in one pass, in one basis
     p = residue_perm(L, residue) if residue else None
     pt = torch.from_numpy(p).long().to(q.device) if p is not None else None
-    qp, kp, vp = ((x[:, pt].contiguous() if pt is not None else x) for x in (q, k, v))
-    dop = torch.randn(qp.shape, generator=torch.Generator().manual_seed(7)).to(q.dtype).to(q.device)
-    # o and lse from this build's forward on the same (relabelled) tensors
-    lse = torch.empty(H, L, dtype=torch.float32, device=q.device)
-    bi = pindex.build(wl.union, L, 64, 64, perm=p, device=q.device)
-    launch = pattn.prepare(qp, kp, vp, *pindex.to_cuda(bi, q.device),
-                           device_mask(wl.union, L, q.device, perm=p), 0, 0, 0, 64, 64, lse=lse,
-                           kernel="general")
-    o = launch()
-    plan = pbwd.BackwardPlan(wl.union, L, q.device, perm=p)
-    for _ in range(warmup):
-        plan.backward(qp, kp, vp, o, lse, dop)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-    torch.cuda.synchronize()
-    ev[0].record()
-    for _ in range(reps):
-        plan.backward(qp, kp, vp, o, lse, dop)
-    ev[1].record()
-    torch.cuda.synchronize()
-    ms = ev[0].elapsed_time(ev[1]) / reps
-    live = int(bi.live)
-    tiles = int(plan.kv_num.sum())
+    qp, kp, vp, op, dp = ((x[:, pt].contiguous() if pt is not None else x) for x in (q, k, v, o, dop))
+    lsep = lse[:, pt].contiguous() if pt is not None else lse
+    single = pbwd.BackwardPlan(wl.union, L, q.device, perm=p)
+    ms1 = timed(lambda: single.backward(qp, kp, vp, op, lsep, dp))
+    live = int(split.live)
     fl = 8 * D * live * H
     tf = fl / (ms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[_dt(q.dtype)]
-    return dict(basis=f"rp{residue}" if residue else "identity", tile=64, tiles=tiles, ms=round(ms, 4),
-                live_tflops=round(tf, 2), tile_tflops=round(8 * D * tiles * 64 * 64 * H / (ms * 1e-3) / 1e12, 2),
+    return dict(pieces=[(f"rp{s}" if s else "identity") for s, _, _ in split.steps], tile=64, tiles=tiles,
+                ms=round(ms, 4), live_tflops=round(tf, 2),
+                tile_tflops=round(8 * D * tiles * 64 * 64 * H / (ms * 1e-3) / 1e12, 2),
                 roofline=dict(bound="mfma", achieved=round(tf, 2), peak=peak, unit="TFLOP/s", frac=round(tf / peak, 4)),
-                note="one backward of the whole mask (pre-pass + dK/dV + dQ launches); live FLOP = 8 D per live "
-                     "pair and head, recomputed scores not counted")
+                single_basis=dict(basis=f"rp{residue}" if residue else "identity", tiles=int(single.kv_num.sum()),
+                                  ms=round(ms1, 4), live_tflops=round(fl / (ms1 * 1e-3) / 1e12, 2)),
+                note="backward of the whole mask from the forward's o and lse, split into the forward's pieces "
+                     "(gathers and scatters of the permuted pieces included); live FLOP = 8 D per live pair and "
+                     "head, recomputed scores not counted")
 
 
 def cpu_baseline(wl, budget_s=12.0):
@@ -336,7 +341,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     permute = measure_permute(q, k, v, residues[0]) if residues and variant is None else None
     decode = (measure_decode(wl, q, k, v, (0,) + tuple(sorted(set(residues))))
               if variant is None and wl.D in (64, 128) and wl.dtype != torch.float32 else None)
-    backward = (measure_backward(wl, q, k, v, max(residues) if residues else 0)
+    backward = (measure_backward(wl, q, k, v, o, lse, max(residues) if residues else 0)
                 if variant is None and wl.D in (64, 128) and wl.dtype != torch.float32 and wl.L % 64 == 0 else None)
     kernels = ["attn_stream_kernel" if x.kernel == "stream" else "attn_fwd_kernel" for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch

@@ -299,7 +299,17 @@ int pa_decode_fwd(const pa_decode_args* args, void* stream);
  * dvec is a caller-owned fp32 [BH, N] workspace (rowsum(dO * O), same stride as lse).
  * kv_bits_off / kv_bits (pa_index_bits) with q_bits_off / q_bits (their transpose) are
  * all NULL or all given; given, the D = 128 kernels mask partial tiles from them instead
- * of evaluating the mask. */
+ * of evaluating the mask.  flags: PA_BWD_ACCUMULATE adds the gradients into dq / dk / dv
+ * instead of overwriting them (the backward of a mask split into disjoint pieces is the
+ * sum of the pieces' backwards, each with the whole mask's lse and dvec);
+ * PA_BWD_DVEC_GIVEN takes dvec as already holding rowsum(dO * O) (no pre-pass).
+ * residue_s > 1 (D = 128, N / s a power of two and a multiple of 64): the index is in the
+ * residue-s basis but q, k, v, o, dout, lse, dvec and the gradients stay in ORIGINAL
+ * order; index-space row r is read and written at row (r mod (N/s)) s + r div (N/s)
+ * (the basis applied in the loads and stores, as gather_q / gather_kv / scatter_o do in
+ * the forward).  0 = every array in index space. */
+#define PA_BWD_ACCUMULATE 1
+#define PA_BWD_DVEC_GIVEN 2
 int pa_index_transpose(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
                        const int32_t* kv_bits_off, int32_t nq, int64_t pitch, int32_t nk, int32_t* q_num,
                        int32_t* q_idx, int8_t* q_partial, int32_t* q_bits_off, int64_t tpitch, void* stream);
@@ -335,6 +345,8 @@ typedef struct pa_attn_bwd_args {
   const uint32_t* kv_bits;
   const int32_t* q_bits_off;
   const uint32_t* q_bits;
+  int32_t flags;
+  int32_t residue_s;
   pa_mask mask;
 } pa_attn_bwd_args;
 

@@ -6,6 +6,10 @@ output and row log-sum-exp: dV = P^T dO, dP = dO V^T, dS = P (dP - rowsum(dO O))
 dQ = scale dS K, dK = scale dS^T Q, with P = exp(scale q k^T - lse) on live pairs.
 ``BackwardPlan`` builds the block index at 64 x 64 tiles and its transpose once (on the
 device), then every ``backward`` call is one pre-pass and two kernels (pa_attn_bwd).
+``SplitBackward`` runs a mask split into disjoint pieces, each in its own basis, the
+way the forward's split plan does: the gradients are sums over live pairs, so the
+backward of the union is the sum of the pieces' backwards, each taking the whole mask's
+lse and rowsum(dO O).
 """
 import ctypes
 
@@ -13,9 +17,12 @@ import torch
 
 from . import _lib
 from .index import build_device
+from .perm import permute_rows, permute_stack, residue_perm
 from .spec import DeviceMask, device_mask
 
 TILE = 64
+ACCUMULATE = 1   # PA_BWD_ACCUMULATE
+DVEC_GIVEN = 2   # PA_BWD_DVEC_GIVEN
 
 
 def transpose_index(kv_idx, kv_num, kv_partial, n_kv_blocks, kv_bits_off=None):
@@ -63,18 +70,26 @@ class BackwardPlan:
     perm / perm_kv: index-space position -> original position, when the tensors given to
     ``backward`` are relabelled (the mask is evaluated in original coordinates).
     bitmaps=False leaves out the partial tiles' element bitmaps: the kernels then
-    evaluate the mask on partial tiles."""
+    evaluate the mask on partial tiles.  residue=s > 1 builds the index in the residue-s
+    basis (perm = perm_kv = residue_perm(N, s)), so that ``backward`` can also take the
+    tensors in original order and apply the basis in its loads and stores."""
 
-    def __init__(self, mask, N, device=None, perm=None, perm_kv=None, bitmaps=True):
+    def __init__(self, mask, N, device=None, perm=None, perm_kv=None, bitmaps=True, residue=0):
         if N % TILE:
             raise ValueError(f"N={N} must be a multiple of {TILE}")
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self.N, self.device = N, dev
+        self.residue = int(residue) if residue and residue > 1 else 0
+        if self.residue:
+            if perm is not None or perm_kv is not None:
+                raise ValueError("residue and perm / perm_kv are exclusive")
+            perm = perm_kv = residue_perm(N, self.residue)
         if isinstance(mask, DeviceMask):
             raise ValueError("BackwardPlan takes a mask object (with perm / perm_kv), not a DeviceMask")
         self.dmask = device_mask(mask, N, dev, perm=perm, perm_kv=perm_kv)
         built = build_device(mask, N, TILE, TILE, perm=perm, perm_kv=perm_kv, device=dev, bits=bitmaps)
         kv_idx, kv_num, kv_partial = built[:3]
+        self.live = int(built[5])      # live pairs of the mask (per head)
         self.kv_idx, self.kv_num, self.kv_partial = kv_idx.contiguous(), kv_num.contiguous(), kv_partial.contiguous()
         # element bitmaps of the partial tiles, row-major for the dQ pass and transposed for
         # the dK / dV pass, so neither evaluates the mask
@@ -83,9 +98,14 @@ class BackwardPlan:
             self.kv_idx, self.kv_num, self.kv_partial, N // TILE, self.kv_bits_off)
         self.q_bits = transpose_bits(self.kv_bits_off, self.kv_bits) if bitmaps else None
 
-    def backward(self, q, k, v, o, lse, do, scale=None, dq=None, dk=None, dv=None):
+    def backward(self, q, k, v, o, lse, do, scale=None, dq=None, dk=None, dv=None, dvec=None, dvec_given=False,
+                 accumulate=False, original_order=False):
         """(dq, dk, dv) for [BH, N, D] f16 / bf16 tensors sharing strides; lse float32 [BH, N]
-        from the forward (natural log)."""
+        from the forward (natural log).  dvec: optional float32 [BH, N] buffer for
+        rowsum(dO O) (with dvec_given it already holds it and the pre-pass is skipped).
+        accumulate: add the gradients into dq / dk / dv (which must be given).
+        original_order (a plan built with residue, D = 128): every array is in original
+        order; the kernels read and write through the residue basis."""
         BH, N, D = q.shape
         if N != self.N:
             raise ValueError(f"plan built for N={self.N}, got N={N}")
@@ -104,7 +124,14 @@ class BackwardPlan:
             if t.shape != q.shape or t.dtype != q.dtype or t.stride() != q.stride():
                 raise ValueError(f"{name} must match q in shape, dtype and strides")
             outs.append(t)
-        dvec = torch.empty((BH, N), dtype=torch.float32, device=q.device)
+        if accumulate and (dq is None or dk is None or dv is None):
+            raise ValueError("accumulate needs dq, dk and dv")
+        if dvec is None:
+            if dvec_given:
+                raise ValueError("dvec_given needs dvec")
+            dvec = torch.empty((BH, N), dtype=torch.float32, device=q.device)
+        elif dvec.dtype != torch.float32 or dvec.shape != (BH, N) or dvec.stride() != lse.stride():
+            raise ValueError("dvec must be float32 [BH, N] with lse's strides")
         a = _lib.PaAttnBwdArgs()
         a.q, a.k, a.v, a.o, a.dout = (_lib.ptr(t) for t in ts)
         a.dq, a.dk, a.dv = (_lib.ptr(t) for t in outs)
@@ -119,8 +146,72 @@ class BackwardPlan:
         if self.kv_bits is not None:
             a.kv_bits_off, a.kv_bits = _lib.ptr(self.kv_bits_off), _lib.ptr(self.kv_bits)
             a.q_bits_off, a.q_bits = _lib.ptr(self.q_bits_off), _lib.ptr(self.q_bits)
+        a.flags = (ACCUMULATE if accumulate else 0) | (DVEC_GIVEN if dvec_given else 0)
+        if original_order:
+            if not self.residue:
+                raise ValueError("original_order needs a plan built with residue")
+            a.residue_s = self.residue
         a.mask = self.dmask.struct()
         with torch.cuda.device(q.device):
             _lib.check(_lib.lib().pa_attn_bwd(ctypes.byref(a), _lib.stream_of(q)), "pa_attn_bwd")
         return tuple(outs)
 
+
+def _fusable(N, s):
+    """The residue-s basis can be applied in the backward kernels' loads and stores."""
+    per = N // s
+    return N % s == 0 and per % 64 == 0 and (per & (per - 1)) == 0
+
+
+class SplitBackward:
+    """The backward of a mask split into disjoint pieces (split.Piece: mask and residue;
+    the tile shape is always 64 x 64 here), each piece in its own basis.  Every piece adds
+    into the same gradients in original order: at D = 128 a permuted piece reads and
+    writes through its residue basis inside the kernels (no copies); otherwise its
+    tensors are gathered into the basis and its gradients scattered back, and such pieces
+    run first.  Pieces without a live tile are left out."""
+
+    def __init__(self, pieces, N, device=None):
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.N, self.device = N, dev
+        order = sorted(pieces, key=lambda p: not (p.residue and p.residue > 1))
+        self.steps = []
+        for p in order:
+            s = int(p.residue) if p.residue and p.residue > 1 else 0
+            plan = BackwardPlan(p.mask, N, dev, residue=s)
+            if int(plan.kv_num.sum()):
+                perm = torch.from_numpy(residue_perm(N, s)).to(dev) if s else None
+                self.steps.append((s, perm, plan))
+
+    @property
+    def tiles(self):
+        return sum(int(plan.kv_num.sum()) for _, _, plan in self.steps)
+
+    @property
+    def live(self):
+        return sum(plan.live for _, _, plan in self.steps)
+
+    def backward(self, q, k, v, o, lse, do, scale=None):
+        """(dq, dk, dv) of the union of the pieces, tensors in the original order."""
+        lse = lse.contiguous()
+        if not self.steps:
+            return tuple(torch.zeros_like(q) for _ in range(3))
+        D = q.shape[2]
+        outs, dvec, have = None, torch.empty_like(lse), False
+        for s, perm, plan in self.steps:
+            if s and not (D == 128 and _fusable(self.N, s)):
+                (qp, kp, vp, op, dop), _ = permute_stack([q, k, v, o, do], perm, with_positions=False)
+                lsep = permute_rows(lse, perm)
+                dvp = permute_rows(dvec, perm) if have else torch.empty_like(lsep)
+                tgt = permute_stack(list(outs), perm, with_positions=False)[0] if outs is not None else [None] * 3
+                g = plan.backward(qp, kp, vp, op, lsep, dop, scale, *tgt, dvec=dvp, dvec_given=have,
+                                  accumulate=outs is not None)
+                if not have:
+                    dvec = permute_rows(dvp, perm, inverse=True)
+                outs = permute_stack(list(g), perm, inverse=True, with_positions=False)[0]
+            else:
+                tgt = outs if outs is not None else (None, None, None)
+                outs = plan.backward(q, k, v, o, lse, do, scale, *tgt, dvec=dvec, dvec_given=have,
+                                     accumulate=outs is not None, original_order=bool(s))
+            have = True
+        return tuple(outs)

@@ -58,8 +58,25 @@ struct BwdK {
   const uint32_t* kv_bits;     // 64 rows x 2 words per partial tile, row-major
   const int32_t* q_bits_off;   // [nb, tpitch], same offsets in the transposed lists
   const uint32_t* q_bits;      // the same bitmaps transposed (64 columns x 2 words)
+  int32_t accumulate;          // add into dq / dk / dv
+  // > 0 (D = 128 only): the tensors (and lse, dvec) are in ORIGINAL order and index-space
+  // row r lives at row (r mod 2^qlog2) s + r div 2^qlog2 (the residue-s permutation in
+  // closed form); a 64-row tile is then 64 rows s apart
+  int32_t residue_s, residue_qlog2;
   Pred pred;
 };
+
+// Memory row of index-space row r.
+__device__ __forceinline__ int64_t mem_row(const BwdK& a, int r) {
+  return a.residue_s ? (int64_t)(r & ((1 << a.residue_qlog2) - 1)) * a.residue_s + (r >> a.residue_qlog2) : r;
+}
+
+// 4 gradient elements stored (or added to the stored ones) in the tensor's type.
+template <typename T>
+__device__ __forceinline__ void store_grad4(char* p, f32x4 x, bool acc) {
+  if (acc) x += load4_any(p, __is_same(T, __bf16) ? PA_BF16 : PA_F16);
+  Mma<T>::store4(p, x);
+}
 
 // rowsum(dO * O) of one row per thread, in fp32.
 template <typename T, int D>
@@ -243,8 +260,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1))) void b
       f32x4 xk = {dkt[db][4 * i4], dkt[db][4 * i4 + 1], dkt[db][4 * i4 + 2], dkt[db][4 * i4 + 3]};
       const f32x4 xv = {dvt[db][4 * i4], dvt[db][4 * i4 + 1], dvt[db][4 * i4 + 2], dvt[db][4 * i4 + 3]};
       xk *= a.scale;
-      Mma<T>::store4(dkrow + d0 * ESZ, xk);
-      Mma<T>::store4(dvrow + d0 * ESZ, xv);
+      store_grad4<T>(dkrow + d0 * ESZ, xk, a.accumulate);
+      store_grad4<T>(dvrow + d0 * ESZ, xv, a.accumulate);
     }
   }
 }
@@ -343,7 +360,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void b
       const int d0 = 32 * db + 8 * i4 + 4 * G;
       f32x4 x = {dqt[db][4 * i4], dqt[db][4 * i4 + 1], dqt[db][4 * i4 + 2], dqt[db][4 * i4 + 3]};
       x *= a.scale;
-      Mma<T>::store4(dqrow + d0 * ESZ, x);
+      store_grad4<T>(dqrow + d0 * ESZ, x, a.accumulate);
     }
   }
 }
@@ -421,22 +438,24 @@ __device__ __forceinline__ typename Mma<T>::frag tr_frag_sw(const TileReads& t, 
   return __builtin_bit_cast(typename Mma<T>::frag, vx);
 }
 
-// DMA of rows r0 .. r0 + 63 of two [N, 128] tensors (row pitch rowb bytes, heads already
-// applied) into stage tiles at LDS m0 and m0 + kTB, in four parts (instructions 2 part,
+// DMA of the 64 rows of a tile of two [N, 128] tensors (heads applied; the tile's first
+// row at byte r0b, its rows `pitch` bytes apart: the row pitch, or s times it when the
+// tile is gathered through the residue-s basis) into stage tiles at LDS m0 and m0 + kTB,
+// in four parts (instructions 2 part,
 // 2 part + 1 of each tensor), so that a tile's DMA can be spread over the previous tile's
 // MFMAs.  Wave w moves rows 32 w .. 32 w + 31; its instruction i writes rows
 // 32 w + 4 i + l / 16, lane l unit l % 16, fetching the unit the swizzle stores there:
 // (l % 16) ^ (4 (l / 16) + i % 4) (dvoff[i % 4]).
-__device__ __forceinline__ void dma_tile_part(uint32_t m0, const char* g0, const char* g1, int64_t rowb, int64_t r0,
+__device__ __forceinline__ void dma_tile_part(uint32_t m0, const char* g0, const char* g1, int64_t pitch, int64_t r0b,
                                               int w, const uint32_t* dvoff, int part) {
-  const char* a0 = g0 + (r0 + 32 * w) * rowb;
-  const char* a1 = g1 + (r0 + 32 * w) * rowb;
+  const char* a0 = g0 + r0b + 32 * w * pitch;
+  const char* a1 = g1 + r0b + 32 * w * pitch;
   const uint32_t mw = m0 + (uint32_t)(32 * w * 256);
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii) {
     const int i = 2 * part + ii;
-    dma_x4(mw + i * 1024, a0 + 4 * i * rowb, dvoff[i & 3]);
-    dma_x4(mw + kTB + i * 1024, a1 + 4 * i * rowb, dvoff[i & 3]);
+    dma_x4(mw + i * 1024, a0 + 4 * i * pitch, dvoff[i & 3]);
+    dma_x4(mw + kTB + i * 1024, a1 + 4 * i * pitch, dvoff[i & 3]);
   }
 }
 
@@ -460,7 +479,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int64_t bh = id / a.nb;
   const int key = kb * kBT + w * 32 + m;
   const int key_o = orig_of(a.pred.perm_kv, key);
+  const int64_t key_m = mem_row(a, key);
   const int64_t rowb = a.sn * ESZ;
+  const int rs = a.residue_s ? a.residue_s : 1;  // memory rows between a tile's rows
+  const int64_t pitch = rs * rowb;
   const char* hq = a.q + bh * a.sb * ESZ;
   const char* hdo = a.dout + bh * a.sb * ESZ;
   const char* hlse = reinterpret_cast<const char*>(a.lse + bh * a.lse_sb);
@@ -470,20 +492,21 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   uint32_t dvoff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    dvoff[j] = (uint32_t)((lane >> 4) * rowb) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
+    dvoff[j] = (uint32_t)((lane >> 4) * pitch) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
   const bool use_bits = a.q_bits != nullptr;
   // query block qb into stage S: Q and dO tiles; lse (and, without bitmaps, the original
   // row numbers) by wave 0, rowsum(dO O) by wave 1; a partial tile's bitmap (bo >= 0),
   // columns 32 w .. 32 w + 31 by wave w
   auto dma = [&](int qb, int bo, int S, int part) __attribute__((always_inline)) {
-    dma_tile_part(lds0 + S * kStage, hq, hdo, rowb, (int64_t)qb * kBT, w, dvoff, part);
+    const int64_t r0 = mem_row(a, qb * kBT);
+    dma_tile_part(lds0 + S * kStage, hq, hdo, pitch, r0 * rowb, w, dvoff, part);
     if (part) return;
     const uint32_t mv = lds0 + kVecOff + S * kVec;
     if (w == 0) {
-      dma_x1(mv, hlse + (int64_t)qb * 256, 4u * lane);
+      dma_x1(mv, hlse + r0 * 4, 4u * rs * lane);
       if (hperm && !use_bits) dma_x1(mv + 512, hperm + (int64_t)qb * 256, 4u * lane);
     } else {
-      dma_x1(mv + 256, hdvec + (int64_t)qb * 256, 4u * lane);
+      dma_x1(mv + 256, hdvec + r0 * 4, 4u * rs * lane);
     }
     if (use_bits && bo >= 0)
       dma_x1(mv + kBitsAt + 256 * w, reinterpret_cast<const char*>(a.q_bits + bo) + 256 * w, 4u * lane);
@@ -493,8 +516,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   lds_cptr vrow = lds + kVecOff + 16 * G;  // lse of rows 8 j + 4 G + 0..3 (+ 32 lb)
 
   Frag kf[NKC], vf[NKC];
-  row_frags<T, 128>(a.k + (bh * a.sb + (int64_t)key * a.sn) * ESZ + 16 * G, kf);
-  row_frags<T, 128>(a.v + (bh * a.sb + (int64_t)key * a.sn) * ESZ + 16 * G, vf);
+  row_frags<T, 128>(a.k + (bh * a.sb + key_m * a.sn) * ESZ + 16 * G, kf);
+  row_frags<T, 128>(a.v + (bh * a.sb + key_m * a.sn) * ESZ + 16 * G, vf);
   f32x16 dkt[NDB], dvt[NDB];
 #pragma unroll
   for (int i = 0; i < NDB; ++i) dkt[i] = dvt[i] = f32x16{0};
@@ -690,8 +713,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   if (t < nl) step(std::integral_constant<int, 0>{}, t);
 
   // dK^T / dV^T blocks [32 d x 32 keys]: lane (key m, G) holds d = 32 db + 8 i4 + 4 G + 0..3
-  char* dkrow = a.dk + (bh * a.sb + (int64_t)key * a.sn) * ESZ;
-  char* dvrow = a.dv + (bh * a.sb + (int64_t)key * a.sn) * ESZ;
+  char* dkrow = a.dk + (bh * a.sb + key_m * a.sn) * ESZ;
+  char* dvrow = a.dv + (bh * a.sb + key_m * a.sn) * ESZ;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -700,8 +723,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       f32x4 xk = {dkt[db][4 * i4], dkt[db][4 * i4 + 1], dkt[db][4 * i4 + 2], dkt[db][4 * i4 + 3]};
       const f32x4 xv = {dvt[db][4 * i4], dvt[db][4 * i4 + 1], dvt[db][4 * i4 + 2], dvt[db][4 * i4 + 3]};
       xk *= a.scale;
-      Mma<T>::store4(dkrow + d0 * ESZ, xk);
-      Mma<T>::store4(dvrow + d0 * ESZ, xv);
+      store_grad4<T>(dkrow + d0 * ESZ, xk, a.accumulate);
+      store_grad4<T>(dvrow + d0 * ESZ, xv, a.accumulate);
     }
   }
 }
@@ -725,7 +748,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int64_t bh = id / a.nb;
   const int row = qb * kBT + w * 32 + m;  // this lane's query row (index space)
   const int q_o = orig_of(a.pred.perm_q, row);
+  const int64_t row_m = mem_row(a, row);
   const int64_t rowb = a.sn * ESZ;
+  const int rs = a.residue_s ? a.residue_s : 1;
+  const int64_t pitch = rs * rowb;
   const char* hk = a.k + bh * a.sb * ESZ;
   const char* hv = a.v + bh * a.sb * ESZ;
   const char* hperm = reinterpret_cast<const char*>(a.pred.perm_kv);
@@ -733,12 +759,12 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   uint32_t dvoff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    dvoff[j] = (uint32_t)((lane >> 4) * rowb) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
+    dvoff[j] = (uint32_t)((lane >> 4) * pitch) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
   const bool use_bits = a.kv_bits != nullptr;
   // key block kb into stage S: K and V tiles; without bitmaps the original key numbers by
   // wave 0; a partial tile's bitmap (bo >= 0), rows 32 w .. 32 w + 31 by wave w
   auto dma = [&](int kb, int bo, int S, int part) __attribute__((always_inline)) {
-    dma_tile_part(lds0 + S * kStage, hk, hv, rowb, (int64_t)kb * kBT, w, dvoff, part);
+    dma_tile_part(lds0 + S * kStage, hk, hv, pitch, mem_row(a, kb * kBT) * rowb, w, dvoff, part);
     if (part) return;
     const uint32_t mv = lds0 + kVecOff + S * kVec;
     if (hperm && !use_bits && w == 0) dma_x1(mv + 512, hperm + (int64_t)kb * 256, 4u * lane);
@@ -749,12 +775,12 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const TileReads rd = tile_reads(lds, lane);
 
   Frag qf[NKC], df[NKC];
-  row_frags<T, 128>(a.q + (bh * a.sb + (int64_t)row * a.sn) * ESZ + 16 * G, qf);
-  row_frags<T, 128>(a.dout + (bh * a.sb + (int64_t)row * a.sn) * ESZ + 16 * G, df);
-  const float lse = a.lse[bh * a.lse_sb + row];
+  row_frags<T, 128>(a.q + (bh * a.sb + row_m * a.sn) * ESZ + 16 * G, qf);
+  row_frags<T, 128>(a.dout + (bh * a.sb + row_m * a.sn) * ESZ + 16 * G, df);
+  const float lse = a.lse[bh * a.lse_sb + row_m];
   const float nl2 = -lse * 1.4426950408889634f;
   const bool dead = lse == -INFINITY;
-  const float dr = a.dvec[bh * a.lse_sb + row];
+  const float dr = a.dvec[bh * a.lse_sb + row_m];
   f32x16 dqt[NDB];
 #pragma unroll
   for (int i = 0; i < NDB; ++i) dqt[i] = f32x16{0};
@@ -915,7 +941,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   if (t < nl) step(std::integral_constant<int, 0>{}, t);
 
-  char* dqrow = a.dq + (bh * a.sb + (int64_t)row * a.sn) * ESZ;
+  char* dqrow = a.dq + (bh * a.sb + row_m * a.sn) * ESZ;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -923,7 +949,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int d0 = 32 * db + 8 * i4 + 4 * G;
       f32x4 x = {dqt[db][4 * i4], dqt[db][4 * i4 + 1], dqt[db][4 * i4 + 2], dqt[db][4 * i4 + 3]};
       x *= a.scale;
-      Mma<T>::store4(dqrow + d0 * ESZ, x);
+      store_grad4<T>(dqrow + d0 * ESZ, x, a.accumulate);
     }
   }
 }
@@ -976,10 +1002,12 @@ __global__ __launch_bounds__(64) void bits_transpose_kernel(const int32_t* kv_bi
 }
 
 template <typename T, int D>
-int launch_bwd(const BwdK& k, int64_t BH, hipStream_t s) {
+int launch_bwd(const BwdK& k, int64_t BH, bool dvec_given, hipStream_t s) {
   const int64_t rows = BH * k.N;
-  hipLaunchKernelGGL((bwd_pre_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, k, rows);
-  PA_LAUNCH_CHECK("bwd_pre_kernel");
+  if (!dvec_given) {
+    hipLaunchKernelGGL((bwd_pre_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, k, rows);
+    PA_LAUNCH_CHECK("bwd_pre_kernel");
+  }
   if constexpr (D == 128) {
     // the dynamic LDS limit is raised once per device
     static unsigned long long configured = 0ull;
@@ -1094,8 +1122,24 @@ extern "C" int pa_attn_bwd(const pa_attn_bwd_args* x, void* stream) {
   k.kv_bits = x->kv_bits;
   k.q_bits_off = x->q_bits_off;
   k.q_bits = x->q_bits;
+  PA_CHECK_ARG((x->flags & ~(PA_BWD_ACCUMULATE | PA_BWD_DVEC_GIVEN)) == 0, "pa_attn_bwd: unknown flags %d", x->flags);
+  k.accumulate = (x->flags & PA_BWD_ACCUMULATE) != 0;
+  k.residue_s = 0;
+  k.residue_qlog2 = 0;
+  if (x->residue_s > 1) {
+    const int64_t per = x->N / x->residue_s;
+    PA_CHECK_ARG(x->D == 128 && x->N % x->residue_s == 0 && (per & (per - 1)) == 0 && per % 64 == 0,
+                 "pa_attn_bwd: residue_s=%d needs D = 128 and N / s a power of two and a multiple of 64 (N=%lld)",
+                 x->residue_s, (long long)x->N);
+    PA_CHECK_ARG((int64_t)x->residue_s * x->sn * 2 * 4 < (1ll << 32), "pa_attn_bwd: residue_s=%d rows too far apart",
+                 x->residue_s);
+    k.residue_s = x->residue_s;
+    while ((1ll << k.residue_qlog2) < per) ++k.residue_qlog2;
+  }
+  const bool dg = (x->flags & PA_BWD_DVEC_GIVEN) != 0;
   k.pred = pa::make_pred(x->mask);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (x->dtype == PA_BF16) return x->D == 128 ? pa::launch_bwd<__bf16, 128>(k, x->BH, s) : pa::launch_bwd<__bf16, 64>(k, x->BH, s);
-  return x->D == 128 ? pa::launch_bwd<_Float16, 128>(k, x->BH, s) : pa::launch_bwd<_Float16, 64>(k, x->BH, s);
+  if (x->dtype == PA_BF16)
+    return x->D == 128 ? pa::launch_bwd<__bf16, 128>(k, x->BH, dg, s) : pa::launch_bwd<__bf16, 64>(k, x->BH, dg, s);
+  return x->D == 128 ? pa::launch_bwd<_Float16, 128>(k, x->BH, dg, s) : pa::launch_bwd<_Float16, 64>(k, x->BH, dg, s);
 }

@@ -15,6 +15,7 @@ from polyhedral_amd import backward as pbwd
 from polyhedral_amd import index as pindex
 from polyhedral_amd.polyattn import masks as pm
 from polyhedral_amd.registry import numpy_mask, triton_params
+from polyhedral_amd.split import Piece
 from tests.util import as64, make_qkv
 
 pytestmark = pytest.mark.gpu
@@ -144,3 +145,55 @@ def test_dead_rows_and_transposed_index(gpu):
             assert np.array_equal(rows, M[qb * 64:qb * 64 + 64, kb * 64:kb * 64 + 64])
             assert np.array_equal(cols.T, rows)
     assert n_partial > 0
+
+
+def test_split_backward_equals_oracle(gpu):
+    """band-256 | lattice-16 split as the forward splits it: the band in the identity basis,
+    the lattice minus the band in rp16.  The gradients are the union's, from fewer tiles."""
+    BH, N, D, name = 2, 1024, 128, "band256+lat16"
+    band = pm.SlidingWindow(256)
+    split = pbwd.SplitBackward([Piece(band), Piece(pm.Difference(pm.Dilated(16), band), residue=16)], N, gpu)
+    q, k, v = make_qkv(BH, N, D, torch.bfloat16, seed=9)
+    do = make_qkv(BH, N, D, torch.bfloat16, seed=10)[0]
+    o, lse, want = _oracle(q, k, v, do, oatt.spec_rows(om.NAMED[name], N))
+    grads = split.backward(q.to(gpu), k.to(gpu), v.to(gpu), torch.from_numpy(o).to(torch.bfloat16).to(gpu),
+                           torch.from_numpy(lse).float().to(gpu), do.to(gpu))
+    _check(grads, want, torch.bfloat16, "split: band + rp16 lattice")
+    single = pbwd.BackwardPlan(numpy_mask(name), N, gpu, perm=op.residue_perm(N, 16))
+    assert split.tiles < int(single.kv_num.sum())
+
+
+def test_split_backward_two_permuted_pieces(gpu):
+    """window-128 (identity) + dilated-16 minus the window (rp16) + dilated-24 minus both
+    (rp8): the second permuted piece adds into gradients gathered into its basis."""
+    BH, N, D = 2, 1024, 128
+    win, lat16 = pm.SlidingWindow(128), pm.Dilated(16)
+    pieces = [Piece(win), Piece(pm.Difference(lat16, win), residue=16),
+              Piece(pm.Difference(pm.Dilated(24), pm.Union(win, lat16)), residue=8)]
+    split = pbwd.SplitBackward(pieces, N, gpu)
+    spec = (((om.WINDOW, 128, 0, 0), (om.DILATED, 16, 0, 0), (om.DILATED, 24, 0, 0)), ())
+    q, k, v = make_qkv(BH, N, D, torch.float16, seed=11)
+    do = make_qkv(BH, N, D, torch.float16, seed=12)[0]
+    o, lse, want = _oracle(q, k, v, do, oatt.spec_rows(spec, N))
+    grads = split.backward(q.to(gpu), k.to(gpu), v.to(gpu), torch.from_numpy(o).to(torch.float16).to(gpu),
+                           torch.from_numpy(lse).float().to(gpu), do.to(gpu))
+    _check(grads, want, torch.float16, "split: three pieces, two permuted")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_residue_basis_in_the_loads_and_stores(gpu, dtype):
+    """A plan in the rp16 basis run on tensors in original order (the kernels read and
+    write through the closed-form permutation) gives the original-order gradients, and
+    accumulate adds onto what the gradients held."""
+    BH, N, D, name = 2, 1024, 128, "band256+lat16"
+    q, k, v = make_qkv(BH, N, D, dtype, seed=13)
+    do = make_qkv(BH, N, D, dtype, seed=14)[0]
+    o, lse, want = _oracle(q, k, v, do, oatt.spec_rows(om.NAMED[name], N))
+    plan = pbwd.BackwardPlan(numpy_mask(name), N, gpu, residue=16)
+    args = [x.to(gpu) for x in (q, k, v)] + [torch.from_numpy(o).to(dtype).to(gpu),
+                                             torch.from_numpy(lse).float().to(gpu), do.to(gpu)]
+    grads = plan.backward(*args, original_order=True)
+    _check(grads, want, dtype, f"rp16 basis in the kernels {dtype}")
+    base = [torch.full_like(args[0], 0.5) for _ in range(3)]
+    acc = plan.backward(*args, dq=base[0], dk=base[1], dv=base[2], accumulate=True, original_order=True)
+    _check([g - 0.5 for g in acc], want, dtype, f"accumulated {dtype}")
