@@ -307,7 +307,10 @@ int pa_decode_fwd(const pa_decode_args* args, void* stream);
  * residue-s basis but q, k, v, o, dout, lse, dvec and the gradients stay in ORIGINAL
  * order; index-space row r is read and written at row (r mod (N/s)) s + r div (N/s)
  * (the basis applied in the loads and stores, as gather_q / gather_kv / scatter_o do in
- * the forward).  0 = every array in index space. */
+ * the forward).  0 = every array in index space.
+ * kv_order: NULL, or the N / 64 key blocks in the order the dK / dV pass issues them
+ * (longest transposed list first balances masks whose few key blocks are held by many
+ * query blocks, such as attention sinks). */
 #define PA_BWD_ACCUMULATE 1
 #define PA_BWD_DVEC_GIVEN 2
 int pa_index_transpose(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* kv_partial,
@@ -347,6 +350,7 @@ typedef struct pa_attn_bwd_args {
   const uint32_t* q_bits;
   int32_t flags;
   int32_t residue_s;
+  const int32_t* kv_order;
   pa_mask mask;
 } pa_attn_bwd_args;
 

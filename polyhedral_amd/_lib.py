@@ -14,7 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libpolyattn_amd.s
 PA_OK, PA_E_INVALID, PA_E_HIP, PA_E_UNSUPPORTED = 0, -1, -2, -3
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 MAX_TERMS = 8
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -61,7 +61,7 @@ class PaAttnBwdArgs(ctypes.Structure):
                 ("D", c_i32), ("dtype", c_i32), ("scale", c_f32),
                 ("kv_idx", c_vp), ("kv_num", c_vp), ("kv_partial", c_vp), ("pitch", c_i64),
                 ("q_idx", c_vp), ("q_num", c_vp), ("q_partial", c_vp), ("tpitch", c_i64),
-                ("kv_bits_off", c_vp), ("kv_bits", c_vp), ("q_bits_off", c_vp), ("q_bits", c_vp), ("flags", c_i32), ("residue_s", c_i32),
+                ("kv_bits_off", c_vp), ("kv_bits", c_vp), ("q_bits_off", c_vp), ("q_bits", c_vp), ("flags", c_i32), ("residue_s", c_i32), ("kv_order", c_vp),
                 ("mask", PaMask)]
 
 

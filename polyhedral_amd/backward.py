@@ -97,6 +97,8 @@ class BackwardPlan:
         self.q_idx, self.q_num, self.q_partial, self.q_bits_off = transpose_index(
             self.kv_idx, self.kv_num, self.kv_partial, N // TILE, self.kv_bits_off)
         self.q_bits = transpose_bits(self.kv_bits_off, self.kv_bits) if bitmaps else None
+        # the dK / dV pass issues the key blocks with the longest lists first
+        self.kv_order = torch.argsort(self.q_num, descending=True, stable=True).to(torch.int32).contiguous()
 
     def backward(self, q, k, v, o, lse, do, scale=None, dq=None, dk=None, dv=None, dvec=None, dvec_given=False,
                  accumulate=False, original_order=False):
@@ -147,6 +149,7 @@ class BackwardPlan:
             a.kv_bits_off, a.kv_bits = _lib.ptr(self.kv_bits_off), _lib.ptr(self.kv_bits)
             a.q_bits_off, a.q_bits = _lib.ptr(self.q_bits_off), _lib.ptr(self.q_bits)
         a.flags = (ACCUMULATE if accumulate else 0) | (DVEC_GIVEN if dvec_given else 0)
+        a.kv_order = _lib.ptr(self.kv_order)
         if original_order:
             if not self.residue:
                 raise ValueError("original_order needs a plan built with residue")

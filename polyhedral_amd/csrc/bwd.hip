@@ -8,17 +8,18 @@
 // Rows with no live key have P = 0 and get no gradient.
 //
 // Tiles are 64 x 64 (query block x key block), from the block index built at
-// BQ = A = 64 and its transpose (pa_index_transpose).  Two kernels, no atomics:
-//  * bwd_dkdv_kernel: one work-group of 2 waves per (key block, head), wave w owning 32
-//    keys.  Its K and V rows stay in registers; per listed query block the Q and dO
-//    rows (plus lse and rowsum(dO * O)) are staged in LDS, S = Q K^T and dP = dO V^T come
-//    out with the wave's keys along the lanes, and dV^T += dO^T P, dK^T += Q^T dS use
-//    transposed LDS reads of dO and Q.
-//  * bwd_dq_kernel: one work-group of 2 waves per (query block, head), the same with the
-//    roles of queries and keys exchanged (the forward's layout): S^T = K Q^T,
-//    dP^T = V dO^T, dQ^T += K^T dS^T.
-// Both evaluate the mask on partial tiles only, in original coordinates (perm_q /
-// perm_kv map index-space rows to them, as in the forward).
+// BQ = A = 64 and its transpose (pa_index_transpose).  Two passes, no atomics:
+//  * dK / dV, per (key block, head): S = Q K^T and dP = dO V^T come out with the keys
+//    along the lanes, and dV^T += dO^T P, dK^T += Q^T dS use transposed LDS reads of dO
+//    and Q.  D = 64: bwd_dkdv_kernel, 2 waves of 32 keys, tiles staged through registers.
+//    D = 128: bwd_dkdv_pair_kernel, 4 waves, a pair per 32 keys with the two products
+//    split between the pair's waves, tiles by LDS DMA.
+//  * dQ, per (query block, head), the same with the roles of queries and keys exchanged
+//    (the forward's layout): S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.  D = 64:
+//    bwd_dq_kernel; D = 128: bwd_dq_stream_kernel (tiles by LDS DMA).
+// Partial tiles are masked from element bitmaps when given (D = 128), else by evaluating
+// the mask in original coordinates (perm_q / perm_kv map index-space rows to them, as in
+// the forward).
 #include <math.h>
 
 #include <type_traits>
@@ -63,6 +64,7 @@ struct BwdK {
   // row r lives at row (r mod 2^qlog2) s + r div 2^qlog2 (the residue-s permutation in
   // closed form); a 64-row tile is then 64 rows s apart
   int32_t residue_s, residue_qlog2;
+  const int32_t* kv_order;     // issue order of the key blocks in the dK / dV pass, or NULL
   Pred pred;
 };
 
@@ -441,9 +443,8 @@ __device__ __forceinline__ typename Mma<T>::frag tr_frag_sw(const TileReads& t, 
 // DMA of the 64 rows of a tile of two [N, 128] tensors (heads applied; the tile's first
 // row at byte r0b, its rows `pitch` bytes apart: the row pitch, or s times it when the
 // tile is gathered through the residue-s basis) into stage tiles at LDS m0 and m0 + kTB,
-// in four parts (instructions 2 part,
-// 2 part + 1 of each tensor), so that a tile's DMA can be spread over the previous tile's
-// MFMAs.  Wave w moves rows 32 w .. 32 w + 31; its instruction i writes rows
+// in four parts (instructions 2 part, 2 part + 1 of each tensor: with 4 waves each moves
+// two parts).  Wave w moves rows 32 w .. 32 w + 31; its instruction i writes rows
 // 32 w + 4 i + l / 16, lane l unit l % 16, fetching the unit the swizzle stores there:
 // (l % 16) ^ (4 (l / 16) + i % 4) (dvoff[i % 4]).
 __device__ __forceinline__ void dma_tile_part(uint32_t m0, const char* g0, const char* g1, int64_t pitch, int64_t r0b,
@@ -459,227 +460,196 @@ __device__ __forceinline__ void dma_tile_part(uint32_t m0, const char* g0, const
   }
 }
 
+// ---------------------------------------------------------------------------------
+// dK / dV (D = 128) with a key group's two products split over a pair of waves, so that
+// a wave holds half the state (one of K / V, one of dK / dV: about 200 registers) and
+// two waves share each SIMD.  Work-group: 4 waves, 64 keys; pair p owns keys
+// 32 p .. 32 p + 31.  Per tile (one listed query block, staged as in the kernels above):
+//   role 0: S = Q K^T, P = exp(scale S - lse) (masked), P to LDS; dV^T += dO^T P;
+//   role 1: dP = dO V^T; with P from LDS, dS = P (dP - rowsum(dO O)); dK^T += Q^T dS.
+// P goes through LDS in the MFMA operand layout (both roles map key m to lane m), as
+// 2-byte values: dS is formed from the rounded P that the MFMAs also use.
+constexpr int kPairP = kVecOff + 2 * kVec;          // P of both pairs: 2 x 4 KB
+constexpr int kPairTerms = kPairP + 2 * 4096;
+constexpr int kPairSmem = kPairTerms + PA_MAX_TERMS * (int)sizeof(pa_term);
+
 template <typename T>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_dkdv_stream_kernel(const BwdK a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dkdv_pair_kernel(const BwdK a) {
   using Frag = typename Mma<T>::frag;
   constexpr int ESZ = 2, NKC = 8, NDB = 4;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char_t*)smem;
   lds_cptr lds = (lds_cptr)smem;
-  pa_term* terms_s = reinterpret_cast<pa_term*>(smem + kTermsOff);
+  pa_term* terms_s = reinterpret_cast<pa_term*>(smem + kPairTerms);
 #pragma unroll
   for (int i = 0; i < PA_MAX_TERMS; ++i)  // (constant indices into the argument block)
     if (threadIdx.x == i) terms_s[i] = a.pred.terms[i];
 
   const int tid = threadIdx.x, lane = tid & 63, G = lane >> 5, m = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // consecutive key blocks of a head on one XCD: neighbours share their query tiles in L2
+  const int pair = w >> 1, role = w & 1;
   const int64_t id = xcd_remap(blockIdx.x, (int64_t)gridDim.x);
-  const int kb = (int)(id % a.nb);
+  const int kr = (int)(id % a.nb);
+  const int kb = a.kv_order ? ((cint*)a.kv_order)[kr] : kr;
   const int64_t bh = id / a.nb;
-  const int key = kb * kBT + w * 32 + m;
+  const int key = kb * kBT + pair * 32 + m;
   const int key_o = orig_of(a.pred.perm_kv, key);
   const int64_t key_m = mem_row(a, key);
   const int64_t rowb = a.sn * ESZ;
-  const int rs = a.residue_s ? a.residue_s : 1;  // memory rows between a tile's rows
+  const int rs = a.residue_s ? a.residue_s : 1;
   const int64_t pitch = rs * rowb;
   const char* hq = a.q + bh * a.sb * ESZ;
   const char* hdo = a.dout + bh * a.sb * ESZ;
   const char* hlse = reinterpret_cast<const char*>(a.lse + bh * a.lse_sb);
   const char* hdvec = reinterpret_cast<const char*>(a.dvec + bh * a.lse_sb);
   const char* hperm = reinterpret_cast<const char*>(a.pred.perm_q);
+  const bool use_bits = a.q_bits != nullptr;
 
   uint32_t dvoff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     dvoff[j] = (uint32_t)((lane >> 4) * pitch) + 16u * (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + j));
-  const bool use_bits = a.q_bits != nullptr;
-  // query block qb into stage S: Q and dO tiles; lse (and, without bitmaps, the original
-  // row numbers) by wave 0, rowsum(dO O) by wave 1; a partial tile's bitmap (bo >= 0),
-  // columns 32 w .. 32 w + 31 by wave w
-  auto dma = [&](int qb, int bo, int S, int part) __attribute__((always_inline)) {
+  // query block qb into stage S: wave w moves rows 16 w .. 16 w + 15 of Q and dO; lse
+  // (and, without bitmaps, the original row numbers) by wave 0, rowsum(dO O) by wave 1,
+  // a partial tile's bitmap (bo >= 0) columns 32 (w - 2) .. +31 by waves 2 and 3
+  auto dma = [&](int qb, int bo, int S) __attribute__((always_inline)) {
     const int64_t r0 = mem_row(a, qb * kBT);
-    dma_tile_part(lds0 + S * kStage, hq, hdo, pitch, r0 * rowb, w, dvoff, part);
-    if (part) return;
+    dma_tile_part(lds0 + S * kStage, hq, hdo, pitch, r0 * rowb, pair, dvoff, 2 * role);
+    dma_tile_part(lds0 + S * kStage, hq, hdo, pitch, r0 * rowb, pair, dvoff, 2 * role + 1);
     const uint32_t mv = lds0 + kVecOff + S * kVec;
     if (w == 0) {
       dma_x1(mv, hlse + r0 * 4, 4u * rs * lane);
       if (hperm && !use_bits) dma_x1(mv + 512, hperm + (int64_t)qb * 256, 4u * lane);
-    } else {
+    } else if (w == 1) {
       dma_x1(mv + 256, hdvec + r0 * 4, 4u * rs * lane);
+    } else if (use_bits && bo >= 0) {
+      dma_x1(mv + kBitsAt + 256 * (w - 2), reinterpret_cast<const char*>(a.q_bits + bo) + 256 * (w - 2), 4u * lane);
     }
-    if (use_bits && bo >= 0)
-      dma_x1(mv + kBitsAt + 256 * w, reinterpret_cast<const char*>(a.q_bits + bo) + 256 * w, 4u * lane);
   };
 
   const TileReads rd = tile_reads(lds, lane);
-  lds_cptr vrow = lds + kVecOff + 16 * G;  // lse of rows 8 j + 4 G + 0..3 (+ 32 lb)
+  lds_cptr vrow = lds + kVecOff + 16 * G;  // row vector entries 8 j + 4 G + 0..3 (+ 32 lb)
+  char* pbuf = smem + kPairP + pair * 4096 + lane * 16;  // this lane's P fragments (+ 1 KB per (lb, c))
 
-  Frag kf[NKC], vf[NKC];
-  row_frags<T, 128>(a.k + (bh * a.sb + key_m * a.sn) * ESZ + 16 * G, kf);
-  row_frags<T, 128>(a.v + (bh * a.sb + key_m * a.sn) * ESZ + 16 * G, vf);
-  f32x16 dkt[NDB], dvt[NDB];
+  // role 0 keeps K and dV, role 1 V and dK
+  Frag kv[NKC];
+  row_frags<T, 128>((role == 0 ? a.k : a.v) + (bh * a.sb + key_m * a.sn) * ESZ + 16 * G, kv);
+  f32x16 acc[NDB];
 #pragma unroll
-  for (int i = 0; i < NDB; ++i) dkt[i] = dvt[i] = f32x16{0};
+  for (int i = 0; i < NDB; ++i) acc[i] = f32x16{0};
 
-  // One tile (stage S): four phases in one straight-line block, the order spelled out for
-  // the scheduler (left alone it waits on every LDS read):
-  //   A  S = Q K^T, dP = dO V^T of query rows 0..31;
-  //   B  the same for rows 32..63, beside the gradient of the scores of rows 0..31;
-  //   C  dV^T += dO^T P, dK^T += Q^T dS of rows 0..31, beside the scores' gradient of 32..63;
-  //   D  dV^T, dK^T of rows 32..63.
-  // Element i of a score block is query row 32 lb + 8 (i / 4) + 4 G + i % 4, key `key`.
-  // pre(k) issues part k of the next tile's DMA (all four before the first MFMA: spread
-  // over the phases they were no faster).
-  auto compute = [&](auto SC, bool partial, int qb, auto&& pre) __attribute__((always_inline)) {
-    constexpr int S = decltype(SC)::value;
-    constexpr int SO = S * kStage;
-    uint32_t live[2] = {0xffffu, 0xffffu};
-    if (partial && use_bits) {
-      // this lane's column of the tile: rows 0..31, 32..63
-      const u32x2 bw = *(lds_u2*)(lds + kVecOff + S * kVec + kBitsAt + (32 * w + m) * 8);
-      const uint32_t b0 = bw.x, b1 = bw.y;
-      live[0] = live16(b0, G);
-      live[1] = live16(b1, G);
-    } else if (partial) {
-      lds_i32* qo = (lds_i32*)(lds + kVecOff + S * kVec + 512);
+  // this lane's 16 x 2 score elements: element i of block lb is query row
+  // 32 lb + 8 (i / 4) + 4 G + i % 4, key `key`
+  auto scores = [&](int SO, int tile_off, f32x16* s) __attribute__((always_inline)) {
 #pragma unroll
-      for (int lb = 0; lb < 2; ++lb) {
-        live[lb] = 0u;
-#pragma unroll 1
-        for (int i = 0; i < 16; ++i) {
-          const int qr = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
-          const int q_o = hperm ? qo[qr] : qb * kBT + qr;
-          if (pred_live_rolled(terms_s, a.pred.n_include, a.pred.n_exclude, q_o, key_o, a.pred.dense_bits,
-                               a.pred.dense_words))
-            live[lb] |= 1u << i;
-        }
-      }
+    for (int lb = 0; lb < 2; ++lb) {
+      u32x4 xa[NKC];
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) xa[kc] = *(lds_u4*)(rd.row[kc] + SO + tile_off + lb * 8192);
+      s[lb] = Mma<T>::mma(__builtin_bit_cast(Frag, xa[0]), kv[0], f32x16{0});
+#pragma unroll
+      for (int kc = 1; kc < NKC; ++kc) s[lb] = Mma<T>::mma(__builtin_bit_cast(Frag, xa[kc]), kv[kc], s[lb]);
     }
-    // scores of rows 32 lb .. +31
-    auto scores = [&](int lb, f32x16& s, f32x16& dp) __attribute__((always_inline)) {
-      u32x4 qa[NKC], da[NKC];
+  };
+  // acc^T += X^T Y for the tile at tile_off (dO for dV, Q for dK), Y = the 4 fragments
+  auto accum = [&](int SO, int tile_off, const Frag* y) __attribute__((always_inline)) {
 #pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) {
-        qa[kc] = *(lds_u4*)(rd.row[kc] + SO + lb * 8192);
-        da[kc] = *(lds_u4*)(rd.row[kc] + SO + kTB + lb * 8192);
-      }
-      s = Mma<T>::mma(__builtin_bit_cast(Frag, qa[0]), kf[0], f32x16{0});
-      dp = Mma<T>::mma(__builtin_bit_cast(Frag, da[0]), vf[0], f32x16{0});
-#pragma unroll
-      for (int kc = 1; kc < NKC; ++kc) {
-        s = Mma<T>::mma(__builtin_bit_cast(Frag, qa[kc]), kf[kc], s);
-        dp = Mma<T>::mma(__builtin_bit_cast(Frag, da[kc]), vf[kc], dp);
-      }
-    };
-    // lse and rowsum(dO O) of the lane's 16 rows of block lb
-    auto vec_reads = [&](int lb, f32x4* l4, f32x4* d4) __attribute__((always_inline)) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        l4[j] = *(lds_f4*)(vrow + S * kVec + (32 * lb + 8 * j) * 4);
-        d4[j] = *(lds_f4*)(vrow + S * kVec + 256 + (32 * lb + 8 * j) * 4);
-      }
-    };
-    // P and dS of rows 32 lb .. +31 as MFMA operands (chunks of 16 rows)
-    auto grads = [&](int lb, const f32x16& s, const f32x16& dp, const f32x4* l4, const f32x4* d4, Frag* pf,
-                     Frag* sf) __attribute__((always_inline)) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        f32x8 pv, sv;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int i = 8 * c + e;
-          const float lse = l4[i >> 2][i & 3];
-          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], a.c, -lse * 1.4426950408889634f));
-          const float p = (((live[lb] >> i) & 1u) && lse != -INFINITY) ? pe : 0.f;
-          pv[e] = p;
-          sv[e] = p * (dp[i] - d4[i >> 2][i & 3]);
-        }
-        pf[c] = Mma<T>::cvt(pv);
-        sf[c] = Mma<T>::cvt(sv);
-      }
-    };
-    // dV^T += dO^T P, dK^T += Q^T dS for rows 32 lb .. +31: the transposed fragments of dO
-    // and Q (chunk c, block db at 4 c + db) are read first, into registers
-    auto tr_reads = [&](int lb, Frag* fd, Frag* fq) __attribute__((always_inline)) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int off = SO + (32 * lb + 16 * c) * 256;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          fd[4 * c + db] = tr_frag_sw<T>(rd, db, off + kTB);
-          fq[4 * c + db] = tr_frag_sw<T>(rd, db, off);
-        }
-      }
-    };
-    auto accum = [&](const Frag* fd, const Frag* fq, const Frag* pf, const Frag* sf) __attribute__((always_inline)) {
+    for (int lb = 0; lb < 2; ++lb) {
+      Frag fx[8];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          dvt[db] = Mma<T>::mma(fd[4 * c + db], pf[c], dvt[db]);
-          dkt[db] = Mma<T>::mma(fq[4 * c + db], sf[c], dkt[db]);
+        for (int db = 0; db < NDB; ++db) fx[4 * c + db] = tr_frag_sw<T>(rd, db, SO + tile_off + (32 * lb + 16 * c) * 256);
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) acc[db] = Mma<T>::mma(fx[4 * c + db], y[2 * lb + c], acc[db]);
+    }
+  };
+
+  auto tile = [&](auto SC, bool partial, int qb) __attribute__((always_inline)) {
+    constexpr int S = decltype(SC)::value;
+    constexpr int SO = S * kStage;
+    if (role == 0) {
+      uint32_t live[2] = {0xffffu, 0xffffu};
+      if (partial && use_bits) {
+        const u32x2 bw = *(lds_u2*)(lds + kVecOff + S * kVec + kBitsAt + (32 * pair + m) * 8);
+        const uint32_t b0 = bw.x, b1 = bw.y;
+        live[0] = live16(b0, G);
+        live[1] = live16(b1, G);
+      } else if (partial) {
+        lds_i32* qo = (lds_i32*)(lds + kVecOff + S * kVec + 512);
+#pragma unroll
+        for (int lb = 0; lb < 2; ++lb) {
+          live[lb] = 0u;
+#pragma unroll 1
+          for (int i = 0; i < 16; ++i) {
+            const int qr = 32 * lb + 8 * (i >> 2) + 4 * G + (i & 3);
+            const int q_o = hperm ? qo[qr] : qb * kBT + qr;
+            if (pred_live_rolled(terms_s, a.pred.n_include, a.pred.n_exclude, q_o, key_o, a.pred.dense_bits,
+                                 a.pred.dense_words))
+              live[lb] |= 1u << i;
+          }
         }
-    };
-    f32x16 s0, dp0, s1, dp1;
-    f32x4 l4a[4], d4a[4], l4b[4], d4b[4];
-    Frag pf0[2], sf0[2], pf1[2], sf1[2], fd[8], fq[8];
-    // A: the row vectors and 4 reads ahead, then one read per MFMA
-    pre(0);
-    pre(1);
-    pre(2);
-    pre(3);
-    vec_reads(0, l4a, d4a);
-    scores(0, s0, dp0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+      }
+      f32x4 l4[2][4];
 #pragma unroll
-    for (int q_ = 0; q_ < 12; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // B: rows 32..63's reads and MFMAs, rows 0..31's gradient in the VALU slots
-    vec_reads(1, l4b, d4b);
-    scores(1, s1, dp1);
-    grads(0, s0, dp0, l4a, d4a, pf0, sf0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+      for (int lb = 0; lb < 2; ++lb)
 #pragma unroll
-    for (int q_ = 0; q_ < 12; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-    }
+        for (int j = 0; j < 4; ++j) l4[lb][j] = *(lds_f4*)(vrow + S * kVec + (32 * lb + 8 * j) * 4);
+      f32x16 s[2];
+      scores(SO, 0, s);
+      Frag pf[4];
 #pragma unroll
-    for (int q_ = 0; q_ < 4; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // C: all transposed reads of rows 0..31 first, then their MFMAs with rows 32..63's
-    // gradient in the VALU slots
-    tr_reads(0, fd, fq);
-    grads(1, s1, dp1, l4b, d4b, pf1, sf1);
-    accum(fd, fq, pf0, sf0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 32, 0);
+      for (int lb = 0; lb < 2; ++lb)
 #pragma unroll
-    for (int q_ = 0; q_ < 16; ++q_) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
+        for (int c = 0; c < 2; ++c) {
+          f32x8 pv;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int i = 8 * c + e;
+            const float lse = l4[lb][i >> 2][i & 3];
+            const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[lb][i], a.c, -lse * 1.4426950408889634f));
+            pv[e] = (((live[lb] >> i) & 1u) && lse != -INFINITY) ? pe : 0.f;
+          }
+          pf[2 * lb + c] = Mma<T>::cvt(pv);
+          *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((lds_char_t*)pbuf + (2 * lb + c) * 1024) =
+              __builtin_bit_cast(u32x4, pf[2 * lb + c]);
+        }
+      __syncthreads();  // P is in LDS
+      accum(SO, kTB, pf);  // dV^T += dO^T P
+    } else {
+      f32x4 d4[2][4];
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d4[lb][j] = *(lds_f4*)(vrow + S * kVec + 256 + (32 * lb + 8 * j) * 4);
+      f32x16 dp[2];
+      scores(SO, kTB, dp);
+      __syncthreads();  // P is in LDS
+      Frag sf[4];
+#pragma unroll
+      for (int lb = 0; lb < 2; ++lb)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const Frag pf = __builtin_bit_cast(Frag, *(lds_u4*)(lds + kPairP + pair * 4096 + lane * 16 + (2 * lb + c) * 1024));
+          const f32x8 pfl = __builtin_convertvector(pf, f32x8);
+          f32x8 sv;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int i = 8 * c + e;
+            sv[e] = pfl[e] * (dp[lb][i] - d4[lb][i >> 2][i & 3]);
+          }
+          sf[2 * lb + c] = Mma<T>::cvt(sv);
+        }
+      accum(SO, 0, sf);  // dK^T += Q^T dS
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // D: rows 32..63
-    tr_reads(1, fd, fq);
-    accum(fd, fq, pf1, sf1);
-    __builtin_amdgcn_sched_group_barrier(0x100, 32, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
   };
 
   const int nl = ((cint*)a.q_num)[kb];
   cint* qlist = (cint*)(a.q_idx + (int64_t)kb * a.tpitch);
   cbyte* plist = (cbyte*)(a.q_partial + (int64_t)kb * a.tpitch);
   cint* olist = (cint*)(use_bits ? a.q_bits_off + (int64_t)kb * a.tpitch : a.q_idx);
-  // listed tile t: query block and bitmap offset (-1: full; without bitmaps 0 = partial)
   auto tile_of = [&](int t, int& qb, int& bo) __attribute__((always_inline)) {
     qb = qlist[t];
     bo = use_bits ? olist[t] : (plist[t] != 0 ? 0 : -1);
@@ -687,23 +657,20 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   int qb_c = 0, bo_c = -1, qb_n = 0, bo_n = -1;
   if (nl > 0) {
     tile_of(0, qb_c, bo_c);
-#pragma unroll
-    for (int part = 0; part < 4; ++part) dma(qb_c, bo_c, 0, part);
+    dma(qb_c, bo_c, 0);
   }
   if (nl > 1) tile_of(1, qb_n, bo_n);
   auto step = [&](auto SC, int t) __attribute__((always_inline)) {
     constexpr int S = decltype(SC)::value;
     dma_wait_all();
-    __syncthreads();  // stage S is in; every wave is past its reads of stage S ^ 1
-    const bool more = t + 1 < nl;
-    const int qb = qb_c, qb_d = qb_n, bo_d = bo_n;
+    __syncthreads();  // stage S is in; every wave is past stage S ^ 1 and the last P
+    if (t + 1 < nl) dma(qb_n, bo_n, S ^ 1);
+    const int qb = qb_c;
     const bool partial = bo_c >= 0;
     qb_c = qb_n;
     bo_c = bo_n;
     if (t + 2 < nl) tile_of(t + 2, qb_n, bo_n);
-    compute(SC, partial, qb, [&](int part) __attribute__((always_inline)) {
-      if (more) dma(qb_d, bo_d, S ^ 1, part);
-    });
+    tile(SC, partial, qb);
   };
   int t = 0;
   for (; t + 1 < nl; t += 2) {
@@ -712,19 +679,18 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   if (t < nl) step(std::integral_constant<int, 0>{}, t);
 
-  // dK^T / dV^T blocks [32 d x 32 keys]: lane (key m, G) holds d = 32 db + 8 i4 + 4 G + 0..3
-  char* dkrow = a.dk + (bh * a.sb + key_m * a.sn) * ESZ;
-  char* dvrow = a.dv + (bh * a.sb + key_m * a.sn) * ESZ;
+  // role 0: dV^T, role 1: dK^T blocks [32 d x 32 keys]: lane (key m, G) holds
+  // d = 32 db + 8 i4 + 4 G + 0..3
+  char* grow = (role == 0 ? a.dv : a.dk) + (bh * a.sb + key_m * a.sn) * ESZ;
+  const float gs = role == 0 ? 1.f : a.scale;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int d0 = 32 * db + 8 * i4 + 4 * G;
-      f32x4 xk = {dkt[db][4 * i4], dkt[db][4 * i4 + 1], dkt[db][4 * i4 + 2], dkt[db][4 * i4 + 3]};
-      const f32x4 xv = {dvt[db][4 * i4], dvt[db][4 * i4 + 1], dvt[db][4 * i4 + 2], dvt[db][4 * i4 + 3]};
-      xk *= a.scale;
-      store_grad4<T>(dkrow + d0 * ESZ, xk, a.accumulate);
-      store_grad4<T>(dvrow + d0 * ESZ, xv, a.accumulate);
+      f32x4 x = {acc[db][4 * i4], acc[db][4 * i4 + 1], acc[db][4 * i4 + 2], acc[db][4 * i4 + 3]};
+      x *= gs;
+      store_grad4<T>(grow + d0 * ESZ, x, a.accumulate);
     }
   }
 }
@@ -1015,8 +981,8 @@ int launch_bwd(const BwdK& k, int64_t BH, bool dvec_given, hipStream_t s) {
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     if (dev >= 64 || !((configured >> dev) & 1ull)) {
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_dkdv_stream_kernel<T>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kBwdSmem);
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_dkdv_pair_kernel<T>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kPairSmem);
       if (e == hipSuccess)
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_dq_stream_kernel<T>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, kBwdSmem);
@@ -1024,8 +990,8 @@ int launch_bwd(const BwdK& k, int64_t BH, bool dvec_given, hipStream_t s) {
       if (dev < 64) configured |= 1ull << dev;
     }
     const unsigned grid = (unsigned)(k.nb * BH);
-    hipLaunchKernelGGL(bwd_dkdv_stream_kernel<T>, dim3(grid), dim3(128), kBwdSmem, s, k);
-    PA_LAUNCH_CHECK("bwd_dkdv_stream_kernel");
+    hipLaunchKernelGGL(bwd_dkdv_pair_kernel<T>, dim3(grid), dim3(256), kPairSmem, s, k);
+    PA_LAUNCH_CHECK("bwd_dkdv_pair_kernel");
     hipLaunchKernelGGL(bwd_dq_stream_kernel<T>, dim3(grid), dim3(128), kBwdSmem, s, k);
     PA_LAUNCH_CHECK("bwd_dq_stream_kernel");
   } else {
@@ -1126,6 +1092,7 @@ extern "C" int pa_attn_bwd(const pa_attn_bwd_args* x, void* stream) {
   k.accumulate = (x->flags & PA_BWD_ACCUMULATE) != 0;
   k.residue_s = 0;
   k.residue_qlog2 = 0;
+  k.kv_order = x->kv_order;
   if (x->residue_s > 1) {
     const int64_t per = x->N / x->residue_s;
     PA_CHECK_ARG(x->D == 128 && x->N % x->residue_s == 0 && (per & (per - 1)) == 0 && per % 64 == 0,
