@@ -445,8 +445,10 @@ def main():
                         for b in dd if isinstance(dd[b], dict)))
                 if r.get("backward"):
                     bw = r["backward"]
-                    log(f"[bench]   backward ({bw['basis']}, 64x64, {bw['tiles']} tiles): {bw['ms']:.3f} ms, "
-                        f"{bw['live_tflops']:.0f} live TFLOP/s ({100 * bw['roofline']['frac']:.1f}%)")
+                    sb = bw["single_basis"]
+                    log(f"[bench]   backward ({' + '.join(bw['pieces'])}, 64x64, {bw['tiles']} tiles): {bw['ms']:.3f} ms, "
+                        f"{bw['live_tflops']:.0f} live TFLOP/s ({100 * bw['roofline']['frac']:.1f}%); one pass in "
+                        f"{sb['basis']} ({sb['tiles']} tiles): {sb['ms']:.3f} ms")
                 if r.get("permute"):
                     pm_ = r["permute"]
                     log(f"[bench]   permute rp{pm_['residue']}: Q/K/V gather {pm_['gather_qkv']['gb_per_s']:.0f} GB/s, "

@@ -80,23 +80,30 @@ __device__ __forceinline__ void store_grad4(char* p, f32x4 x, bool acc) {
   Mma<T>::store4(p, x);
 }
 
-// rowsum(dO * O) of one row per thread, in fp32.
+// rowsum(dO * O) in fp32: a row per D / 8 lanes, 16 bytes of each tensor per lane (the
+// loads of a wave cover whole rows), summed across the row's lanes.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdK a, int64_t rows) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= rows) return;
-  const int64_t bh = r / a.N, i = r - bh * a.N;
-  const char* op = a.o + (bh * a.sb + i * a.sn) * (int64_t)sizeof(T);
-  const char* dp = a.dout + (bh * a.sb + i * a.sn) * (int64_t)sizeof(T);
-  constexpr int DT = __is_same(T, __bf16) ? PA_BF16 : PA_F16;
+  constexpr int LPR = D / 8;  // lanes per row
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t r = g / LPR;
+  const int u = (int)(g % LPR);
   float acc = 0.f;
+  if (r < rows) {
+    const int64_t bh = r / a.N, i = r - bh * a.N;
+    const int64_t off = (bh * a.sb + i * a.sn) * (int64_t)sizeof(T) + 16 * u;
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    const f32x8 x = __builtin_convertvector(*reinterpret_cast<const t8*>(a.o + off), f32x8);
+    const f32x8 y = __builtin_convertvector(*reinterpret_cast<const t8*>(a.dout + off), f32x8);
 #pragma unroll
-  for (int d = 0; d < D; d += 4) {
-    const f32x4 x = load4_any(op + d * sizeof(T), DT);
-    const f32x4 y = load4_any(dp + d * sizeof(T), DT);
-    acc += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(x[e], y[e], acc);
   }
-  a.dvec[bh * a.lse_sb + i] = acc;
+#pragma unroll
+  for (int o = LPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  if (r < rows && u == 0) {
+    const int64_t bh = r / a.N, i = r - bh * a.N;
+    a.dvec[bh * a.lse_sb + i] = acc;
+  }
 }
 
 // LDS pitches of a staged 64-row tile: the K-style pitch (+16 B) serves the 16-byte row
@@ -971,7 +978,8 @@ template <typename T, int D>
 int launch_bwd(const BwdK& k, int64_t BH, bool dvec_given, hipStream_t s) {
   const int64_t rows = BH * k.N;
   if (!dvec_given) {
-    hipLaunchKernelGGL((bwd_pre_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, k, rows);
+    hipLaunchKernelGGL((bwd_pre_kernel<T, D>), dim3((unsigned)((rows * (D / 8) + 255) / 256)), dim3(256), 0, s, k,
+                       rows);
     PA_LAUNCH_CHECK("bwd_pre_kernel");
   }
   if constexpr (D == 128) {
