@@ -80,12 +80,14 @@ def test_product_refuses_host_tensors():
 
 def test_every_struct_field_offset_matches_the_c_compiler(tmp_path):
     """gcc compiles the header and prints offsetof / sizeof of every field of pa_attn_args,
-    pa_mask and pa_term; the ctypes mirrors must agree field by field."""
+    pa_mask, pa_term, pa_decode_args and pa_attn_bwd_args; the ctypes mirrors must agree
+    field by field."""
     import shutil
     import subprocess
     if shutil.which("gcc") is None:
         pytest.skip("gcc not available")
-    structs = {"pa_attn_args": _lib.PaAttnArgs, "pa_mask": _lib.PaMask, "pa_term": _lib.PaTerm}
+    structs = {"pa_attn_args": _lib.PaAttnArgs, "pa_mask": _lib.PaMask, "pa_term": _lib.PaTerm,
+               "pa_decode_args": _lib.PaDecodeArgs, "pa_attn_bwd_args": _lib.PaAttnBwdArgs}
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
@@ -105,3 +107,40 @@ def test_every_struct_field_offset_matches_the_c_compiler(tmp_path):
         assert int(val) == want, f"{cname}.{field}: C {val}, ctypes {want}"
         seen += 1
     assert seen == sum(len(c._fields_) + 1 for c in structs.values())
+
+
+def test_backward_argument_checks_run_before_any_launch():
+    lib = _lib.lib()
+    a = _lib.PaAttnBwdArgs()
+    assert lib.pa_attn_bwd(ctypes.byref(a), None) == _lib.PA_E_INVALID      # dtype 0 (fp32)
+    buf = (ctypes.c_int64 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    for f in ("q", "k", "v", "o", "dout", "dq", "dk", "dv", "lse", "dvec", "kv_idx", "kv_num", "kv_partial",
+              "q_idx", "q_num", "q_partial"):
+        setattr(a, f, p)
+    a.dtype, a.D, a.BH, a.N, a.sb, a.sn, a.pitch, a.tpitch = _lib.PA_BF16, 128, 2, 1024, 1024 * 128, 128, 4, 4
+    a.mask.n_include = 1
+    a.kv_bits = p                                                           # one of four bitmap arrays
+    assert lib.pa_attn_bwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"bitmap" in lib.pa_last_error()
+    a.kv_bits = None
+    a.flags = 4
+    assert lib.pa_attn_bwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"flags" in lib.pa_last_error()
+    a.flags, a.residue_s = 1, 24                                            # 1024 / 24 is not whole
+    assert lib.pa_attn_bwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"residue_s=24" in lib.pa_last_error()
+    a.residue_s, a.D = 16, 64                                               # residue basis needs D = 128
+    assert lib.pa_attn_bwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"residue_s=16" in lib.pa_last_error()
+    a.residue_s, a.N = 0, 1000
+    assert lib.pa_attn_bwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"multiple of 64" in lib.pa_last_error()
+    # the transpose entry points
+    assert lib.pa_index_transpose(p, p, p, None, 0, 4, 16, p, None, None, None, 0, None) == _lib.PA_E_INVALID
+    assert lib.pa_index_transpose(p, p, None, None, 16, 4, 16, p, None, None, None, 0, None) == _lib.PA_E_INVALID
+    assert b"kv_partial" in lib.pa_last_error()
+    assert lib.pa_index_transpose(p, p, p, None, 16, 4, 16, p, p, p, p, 4, None) == _lib.PA_E_INVALID
+    assert b"q_bits_off" in lib.pa_last_error()
+    assert lib.pa_index_bits_transpose(None, 16, 4, p, p, None) == _lib.PA_E_INVALID
+    assert lib.pa_index_bits_transpose(p, 16, 0, None, None, None) == _lib.PA_OK   # nothing listed
