@@ -163,10 +163,13 @@ def test_split_backward_equals_oracle(gpu):
     assert split.tiles < int(single.kv_num.sum())
 
 
-def test_split_backward_two_permuted_pieces(gpu):
+@pytest.mark.parametrize("D", [64, 128])
+def test_split_backward_two_permuted_pieces(gpu, D):
     """window-128 (identity) + dilated-16 minus the window (rp16) + dilated-24 minus both
-    (rp8): the second permuted piece adds into gradients gathered into its basis."""
-    BH, N, D = 2, 1024, 128
+    (rp8).  D = 128 applies the bases inside the kernels; D = 64 gathers the permuted
+    pieces' tensors and scatters their gradients, the second permuted piece adding into
+    gradients gathered into its basis."""
+    BH, N = 2, 1024
     win, lat16 = pm.SlidingWindow(128), pm.Dilated(16)
     pieces = [Piece(win), Piece(pm.Difference(lat16, win), residue=16),
               Piece(pm.Difference(pm.Dilated(24), pm.Union(win, lat16)), residue=8)]
@@ -197,3 +200,14 @@ def test_residue_basis_in_the_loads_and_stores(gpu, dtype):
     base = [torch.full_like(args[0], 0.5) for _ in range(3)]
     acc = plan.backward(*args, dq=base[0], dk=base[1], dv=base[2], accumulate=True, original_order=True)
     _check([g - 0.5 for g in acc], want, dtype, f"accumulated {dtype}")
+
+
+def test_split_backward_of_empty_pieces_is_zero(gpu):
+    N = 1024
+    sub2 = pm.Difference(pm.Dilated(32), pm.PrefixLM(2048))              # empty at N = 1024
+    split = pbwd.SplitBackward([Piece(sub2, residue=32)], N, gpu)
+    assert split.tiles == 0 and split.live == 0
+    q, k, v = (x.to(gpu) for x in make_qkv(1, N, 128, torch.bfloat16, seed=15))
+    lse = torch.full((1, N), -float("inf"), device=gpu)
+    grads = split.backward(q, k, v, torch.zeros_like(q), lse, q)
+    assert all(torch.count_nonzero(g) == 0 for g in grads)
