@@ -1,7 +1,7 @@
 """CPU oracle for the block-sparse attention path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import it,
-and only as the checker (or, for bench.py, the timed CPU baseline).  The product
+and only to check results (or, for bench.py, as the timed CPU baseline).  The product
 (polyhedral_amd) never imports it and has no CPU path.
 
   oracle.masks      predicates of gpu/masks_gpu.py:37-61 (+ PREFIX_LM, difference)

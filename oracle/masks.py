@@ -10,7 +10,7 @@ import numpy as np
 CAUSAL, WINDOW, DILATED, LOCAL_STRIDED, TWOBAND, SINKS, PREFIX_LM, FULL = range(8)
 
 # name -> (include, exclude): the reference's SPECS entries (gpu/masks_gpu.py:11-25)
-# and the BASELINE workloads
+# and the benchmark workloads (band+lattice, sinks+window, prefix-LM+lattice, dilated)
 NAMED = {
     "causal": (((CAUSAL, 0, 0, 0),), ()),
     "window-128": (((WINDOW, 128, 0, 0),), ()),

@@ -290,7 +290,7 @@ class DenseMask(Mask):
 
 def zoo():
     """The masks the reference's test fixture parametrises over (tests/conftest.py:5-7),
-    minus the data-dependent document masks, plus the BASELINE families."""
+    minus the data-dependent document masks, plus the benchmark workloads' families."""
     return [
         Causal(),
         SlidingWindow(128), SlidingWindow(256), SlidingWindow(512), SlidingWindow(1024),

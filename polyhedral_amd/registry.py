@@ -6,7 +6,7 @@ device predicate (kind, p0, p1, p2) or MaskSpec handed to the kernels, and a tor
 mask_mod / dense bool -- checked against each other by check_agreement.  The integer
 kinds 0..5 keep the reference values (gpu/masks_gpu.py:9); PREFIX_LM = 6 is new, and
 entries whose predicate is a union or set difference carry a spec.MaskSpec in the
-kind slot.  The reference's entries are kept and the BASELINE workloads added.
+kind slot.  The reference's entries are kept and the benchmark workloads added.
 """
 import numpy as np
 
@@ -31,7 +31,7 @@ SPECS = {
     "twoband-1000":   (TWOBAND, 128, 1000, 128, lambda: masks.TwoBand(128, 1000)),
     "sinks4+win256":  (SINKS, 256, 4, 0, lambda: masks.SinksWindow(4, 256)),
     "sinks4+win8":    (SINKS, 8, 4, 0, lambda: masks.SinksWindow(4, 8)),
-    # the BASELINE workloads and the pieces of their disjoint splits
+    # the benchmark workloads and the pieces of their disjoint splits
     "window-256":     (WINDOW, 256, 0, 0, lambda: masks.SlidingWindow(256)),
     "dilated-16":     (DILATED, 16, 0, 0, lambda: masks.Dilated(16)),
     "dilated-32":     (DILATED, 32, 0, 0, lambda: masks.Dilated(32)),

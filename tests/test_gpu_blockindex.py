@@ -65,7 +65,7 @@ def test_explicit_matrix_input(gpu):
 
 
 def test_empty_mask_gives_zero_pitch(gpu):
-    # literal BASELINE sub-mask 2: a lattice restricted to pairs a prefix-LM does not cover
+    # a lattice restricted to pairs a prefix-LM does not cover
     N = 4096
     bi = pindex.build(numpy_mask("lat32-prefixlm2048"), N, 128, 32)
     assert bi.kv_idx.shape == (N // 128, 0) and bi.live == 0 and bi.elements == 0

@@ -35,7 +35,7 @@ def test_gather_scatter_exact(gpu, dtype, D):
 
 
 def test_full_size_round_trip(gpu):
-    """BASELINE shape B*H=32, L=16384, D=128, bf16: permute then un-permute is the identity."""
+    """Llama-length shape B*H=32, L=16384, D=128, bf16: permute then un-permute is the identity."""
     BH, N, D = 32, 16384, 128
     x = torch.randn(BH, N, D, device=gpu).to(torch.bfloat16)
     p = pp.residue_perm_device(N, 16, gpu)
