@@ -3,17 +3,24 @@
 
 Default: the L=16384, H=32, D=128 bf16 workload (band-256 | lattice-16, split into
 band-256 in the identity basis and lattice-16 minus band in the rp16 basis, merged
-by log-sum-exp), inputs resident in HBM, one step = one forward over the batch.
-Prints ONE JSON line on stdout (the driver's contract); progress goes to stderr.
+by log-sum-exp), inputs resident in HBM, one step = one forward over the batch;
+then the other four workloads (and the dilated one in both bases) as a per-workload
+block of the same line.  Prints ONE JSON line on stdout (the driver's contract);
+progress goes to stderr.
 
-  python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
-  python bench.py --all [--report PATH]    every workload, a JSON report and a table
+  python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu] [--no-configs]
+  python bench.py --all [--report PATH]    every workload and variant, with every extra
 
-The step times K back-to-back forwards between two device synchronisations.  HIP
-events around each kernel launch give the per-launch durations the roofline uses
-(live FLOPs of the launch / its duration, against the dense MFMA peak).  The CPU
-baseline times the oracle (gpu/reference.py restated: dense masked fp32 attention,
-torch on the host's cores) on a bounded sample of the same workload.
+Each workload first runs forwards back to back for --settle-ms of wall time (the
+GPU's clocks rise over the first ~100 ms of load), then W untimed steps, then K
+timed back-to-back steps between two device synchronisations.  HIP events around
+each kernel launch, on the launch stream, give the per-launch durations the roofline
+uses: live FLOPs of the launch and its algorithmic bytes over its duration, against
+the dense MFMA peak and 8 TB/s; the bound is the one the arithmetic intensity picks.
+After the timed region, the CPU leg times the oracle (gpu/reference.py restated:
+dense masked fp32 attention, torch on the host's cores) on a bounded sample of the
+same workload and checks the timed output against the oracle's float64 attention on
+sampled rows of every head (`parity`).
 """
 import argparse
 import json
@@ -253,16 +260,23 @@ def measure_backward(wl, q, k, v, o, lse, residue, reps=20, warmup=5):
                      "head, recomputed scores not counted")
 
 
-def cpu_baseline(wl, budget_s=12.0):
-    """Oracle dense fp32 attention on the host over (head, 1024-row chunk) units in
-    order until the budget is spent; live-FLOP TFLOP/s over what was processed."""
+def cpu_leg(wl, o, lse, budget_s=12.0, parity_rows=24, seed=11):
+    """The CPU baseline and the parity check, after the timed region.
+
+    cpu_baseline: the oracle's dense masked fp32 attention (gpu/reference.py:5-13 on
+    torch, the host's cores) over (head, chunk-row) units of the same inputs, in order,
+    until `budget_s` is spent; live-FLOP TFLOP/s over what was processed.
+    parity: the timed forward's output `o` (and `lse`) at `parity_rows` sampled query
+    rows of EVERY head against the oracle's float64 dense attention of those rows."""
     import torch
 
     from oracle import attention as oatt
     from oracle import masks as om
     spec = om.NAMED[ORACLE_NAME[wl.name]]
-    q, k, v = (x.float() for x in wl.inputs(0, "cpu"))
+    q, k, v = wl.inputs(0, "cpu")
+    qf, kf, vf = (x.float() for x in (q, k, v))
     chunk = 1024 if wl.L <= 32768 else 512
+    chunk = min(chunk, wl.L)
     units = [(h, r0) for h in range(wl.H) for r0 in range(0, wl.L, chunk)]
     live = 0
     done = 0
@@ -270,18 +284,45 @@ def cpu_baseline(wl, budget_s=12.0):
     for h, r0 in units:
         r1 = min(wl.L, r0 + chunk)
         rows = om.rows(spec, r0, r1, wl.L)
-        oatt.dense_attention_torch(q[h:h + 1, r0:r1].contiguous(), k[h:h + 1], v[h:h + 1],
-                                   lambda a, b, rows=rows, r0=r0: rows[a - 0:b - 0], row_chunk=chunk)
+        oatt.dense_attention_torch(qf[h:h + 1, r0:r1].contiguous(), kf[h:h + 1], vf[h:h + 1],
+                                   lambda a, b, rows=rows: rows[a:b], row_chunk=chunk)
         live += int(rows.sum())
         done += 1
         if time.perf_counter() - t0 > budget_s:
             break
     t = time.perf_counter() - t0
     tflops = 4 * wl.D * live / t / 1e12
-    return dict(value=round(tflops, 6), unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+    base = dict(value=round(tflops, 6), unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
                 sample=f"{done} of {len(units)} (head, {chunk}-row) units of the same inputs, dense masked "
                        f"fp32 attention over all {wl.L} keys (oracle, torch on the host), {t:.1f} s; "
                        f"live pairs in the sample {live}")
+    # parity of the timed output: sampled rows (the first and last rows, block edges, random)
+    rng = np.random.default_rng(seed)
+    fixed = [0, 1, 127, 128, wl.L // 2, wl.L - 1]
+    rows = np.array(sorted(set(fixed) | set(rng.integers(0, wl.L, parity_rows - len(fixed)).tolist())))
+    ws, wl_ = [], []
+    for h in range(wl.H):
+        want, wlse = oatt.dense_attention(qf[h:h + 1, rows].numpy(), kf[h:h + 1].numpy(), vf[h:h + 1].numpy(),
+                                          lambda a, b: om.live(spec, rows[a:b, None].astype(np.int64),
+                                                               np.arange(wl.L)[None, :]),
+                                          row_chunk=len(rows))
+        ws.append(want[0])
+        wl_.append(wlse[0])
+    want = np.stack(ws)
+    wlse = np.stack(wl_)
+    got = o[:, rows].float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - want)
+    glse = lse[:, rows].cpu().numpy().astype(np.float64)
+    fin = np.isfinite(wlse)
+    lse_ok = bool(np.array_equal(np.isfinite(glse), fin))
+    lse_err = float(np.abs(glse[fin] - wlse[fin]).max()) if fin.any() else 0.0
+    tol = {"f32": (1e-5, None), "bf16": (2e-2, 2e-3), "f16": (3e-3, None)}[_dt(wl.dtype)]
+    ok = err.max() <= tol[0] and (tol[1] is None or err.mean() <= tol[1]) and lse_ok
+    parity = dict(max_abs=float(err.max()), mean_abs=float(err.mean()), lse_max_abs=lse_err,
+                  rows=int(len(rows)), heads=wl.H, tol_max=tol[0], tol_mean=tol[1], within_tolerance=bool(ok),
+                  reference="oracle float64 dense masked attention (gpu/reference.py:5-13) of the sampled rows "
+                            "over all keys, every head; the output is the timed forward's")
+    return base, parity
 
 
 def cpu_index_baseline(wl, pieces, gpu_ms, threads=None):
@@ -306,17 +347,68 @@ def cpu_index_baseline(wl, pieces, gpu_ms, threads=None):
 
 
 def _measured_traffic(workload):
-    """HBM bytes per attention launch from the committed counter summary
-    (profiles/attn_traffic_<workload>.json, FETCH_SIZE + WRITE_SIZE scaled by a plain
-    copy of known size), or None if that workload has not been measured."""
+    """HBM bytes per step of the committed counter summary
+    (profiles/attn_traffic_<workload>.json: FETCH_SIZE + WRITE_SIZE per dispatch, each
+    scaled by what the counter reads for a plain copy of known size) with its source,
+    or None if that workload has no summary.  It is not measured in this run."""
     path = os.path.join(ROOT, "profiles", f"attn_traffic_{workload}.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        t = json.load(f)
+    src = (f"profiles/attn_traffic_{workload}.json (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, "
+           f"{t.get('kernel', '?')}, measured at commit {t.get('measured_at_commit', '?')})")
+    return t.get("hbm_bytes_per_step"), src
 
 
-def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
+def settle(launches, min_ms):
+    """Run forwards back to back until `min_ms` of wall time have passed, so the timed
+    steps start on settled clocks (over the first ~100 ms of load the GPU's clocks are
+    still rising, and a few warmup steps time that ramp).  Returns (ms, forwards)."""
+    import torch
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        for _ in range(5):
+            for launch in launches:
+                launch()
+        n += 5
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3
+        if ms >= min_ms:
+            return ms, n
+
+
+def algorithmic_bytes(plan, wl, esz):
+    """Per launch of the plan: Q, K and V rows read once, O and LSE written once; a piece
+    that merges into a previous piece's result also reads that O and LSE once."""
+    t = wl.H * wl.L * wl.D * esz
+    lse = wl.H * wl.L * 4
+    out = []
+    for i, _ in enumerate(plan.launched):
+        rd = 3 * t + (t + lse if i > 0 else 0)
+        out.append(dict(read=rd, write=t + lse))
+    return out
+
+
+def roofline(flops, nbytes, seconds, dt):
+    """Both roofline fractions of `flops` live FLOP moving `nbytes` algorithmic bytes in
+    `seconds`; the bound is the one the arithmetic intensity selects against the ridge
+    (peak FLOP/s over 8 TB/s)."""
+    peak = PEAK_TFLOPS[dt]
+    ridge = peak * 1e12 / (HBM_GBPS * 1e9)
+    inten = flops / nbytes if nbytes else float("inf")
+    tf = flops / seconds / 1e12
+    gbs = nbytes / seconds / 1e9
+    mfma = dict(achieved=round(tf, 3), peak=peak, unit="TFLOP/s", frac=round(tf / peak, 4))
+    hbm = dict(achieved=round(gbs, 1), peak=HBM_GBPS, unit="GB/s", frac=round(gbs / HBM_GBPS, 4),
+               algorithmic_bytes=int(nbytes))
+    bound = "mfma" if inten >= ridge else "hbm"
+    return bound, round(inten, 1), round(ridge, 1), mfma, hbm
+
+
+def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0", extras=True, settle_ms=500.0,
+        cpu_budget=12.0):
     import torch
 
     from polyhedral_amd import workloads
@@ -335,14 +427,22 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
         build_ms.append((time.perf_counter() - t0) * 1e3)
     q, k, v = wl.inputs(0, dev)
     launches, o, lse = plan.prepare(q, k, v)
+    s_ms, s_n = settle(launches, settle_ms)
     wall_ms, per_launch = measure(launches, steps, warmup)
-    iso_ms = measure_isolated(launches, max(25, min(steps, 100)))
+    extras = extras and variant is None
+    iso_ms = measure_isolated(launches, max(25, min(steps, 100))) if extras else None
     residues = [b["piece"].residue for b in plan.built if b["piece"].residue]
-    permute = measure_permute(q, k, v, residues[0]) if residues and variant is None else None
+    permute = measure_permute(q, k, v, residues[0]) if residues and extras else None
     decode = (measure_decode(wl, q, k, v, (0,) + tuple(sorted(set(residues))))
-              if variant is None and wl.D in (64, 128) and wl.dtype != torch.float32 else None)
+              if extras and wl.D in (64, 128) and wl.dtype != torch.float32 else None)
+    if extras or with_cpu:
+        # the timed output, restored after the extra measurements (the decode and backward
+        # legs do not write o / lse, but the isolated forwards rewrite them identically)
+        for launch in launches:
+            launch()
+        torch.cuda.synchronize()
     backward = (measure_backward(wl, q, k, v, o, lse, max(residues) if residues else 0)
-                if variant is None and wl.D in (64, 128) and wl.dtype != torch.float32 and wl.L % 64 == 0 else None)
+                if extras and wl.D in (64, 128) and wl.dtype != torch.float32 and wl.L % 64 == 0 else None)
     kernels = ["attn_stream_kernel" if x.kernel == "stream" else "attn_fwd_kernel" for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
     for i, bi in enumerate(plan.launched):
@@ -354,6 +454,9 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
     dt = _dt(wl.dtype)
     peak = PEAK_TFLOPS[dt]
     achieved = flops_live / (kern_ms * 1e-3) / 1e12
+    ab = algorithmic_bytes(plan, wl, q.element_size())
+    nbytes = sum(x["read"] + x["write"] for x in ab)
+    bound, inten, ridge, mfma, hbm = roofline(flops_live, nbytes, kern_ms * 1e-3, dt)
     res = dict(
         workload=name + (f"[{variant}]" if variant else ""), description=wl.description, dtype=dt,
         H=wl.H, L=wl.L, D=wl.D, live_pairs_per_head=live, tile_elements_per_head=plan.elements,
@@ -364,40 +467,98 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0"):
                      launch_ms=round(per[i], 5),
                      live_tflops=round(4 * wl.D * b["live"] * wl.H / (per[i] * 1e-3) / 1e12, 2) if per[i] else None)
                 for i, b in enumerate(plan.built)],
-        index_build_ms=round(build_ms[1], 2), index_build_cold_ms=round(build_ms[0], 2), ms_per_step=round(wall_ms, 5), kernel_ms=round(kern_ms, 5),
+        index_build_ms=round(build_ms[1], 2), index_build_cold_ms=round(build_ms[0], 2),
+        settle_ms=round(s_ms, 1), settle_forwards=s_n,
+        ms_per_step=round(wall_ms, 5), kernel_ms=round(kern_ms, 5),
         live_tflops=round(flops_live / (wall_ms * 1e-3) / 1e12, 3),
         kernel_live_tflops=round(achieved, 3), tile_tflops=round(flops_tile / (kern_ms * 1e-3) / 1e12, 3),
         peak_tflops=peak, frac_peak=round(achieved / peak, 4),
+        bound=bound, intensity_flop_per_byte=inten, ridge_flop_per_byte=ridge, mfma=mfma, hbm=hbm,
+        algorithmic_bytes=ab,
         min_hbm_bytes=4 * wl.H * wl.L * wl.D * q.element_size(),
     )
     res["hbm_floor_ms"] = round(res["min_hbm_bytes"] / (HBM_GBPS * 1e9) * 1e3, 5)
-    res["isolated"] = dict(ms_median=round(iso_ms, 5), live_tflops=round(flops_live / (iso_ms * 1e-3) / 1e12, 3),
-                           protocol="one forward per event pair after zeroing a 512 MiB buffer, device synchronised "
-                                    "between forwards, median (gpu/bench.py:11-24 with a flush larger than the "
-                                    "memory-side cache)")
+    if iso_ms is not None:
+        res["isolated"] = dict(ms_median=round(iso_ms, 5),
+                               live_tflops=round(flops_live / (iso_ms * 1e-3) / 1e12, 3),
+                               protocol="one forward per event pair after zeroing a 512 MiB buffer, device "
+                                        "synchronised between forwards, median (gpu/bench.py:11-24 with a flush "
+                                        "larger than the memory-side cache)")
     res["permute"] = permute
     res["decode"] = decode
     res["backward"] = backward
     res["_launches"] = len(launches)
     if with_cpu:
-        log(f"[bench] cpu baseline for {name} ...")
-        res["cpu_baseline"] = cpu_baseline(wl)
-        res["index_build"] = cpu_index_baseline(wl, pieces, res["index_build_ms"])
+        log(f"[bench] cpu baseline and parity for {res['workload']} ...")
+        res["cpu_baseline"], res["parity"] = cpu_leg(wl, o, lse, budget_s=cpu_budget)
+        if extras:
+            res["index_build"] = cpu_index_baseline(wl, pieces, res["index_build_ms"])
     del launches, o, lse, q, k, v, plan
     torch.cuda.empty_cache()
     return res
 
 
+def brief(r):
+    """The per-workload entry of the bench line."""
+    out = dict(workload=r["workload"], dtype=r["dtype"], H=r["H"], L=r["L"], D=r["D"],
+               pieces=[f"{p['mask']} {p['BQ']}x{p['A']} {p['basis']}" for p in r["pieces"]],
+               ms_per_step=r["ms_per_step"], kernel_ms=r["kernel_ms"], live_tflops=r["live_tflops"],
+               roofline=dict(bound=r["bound"], intensity_flop_per_byte=r["intensity_flop_per_byte"],
+                             ridge_flop_per_byte=r["ridge_flop_per_byte"], mfma=r["mfma"], hbm=r["hbm"]),
+               waste=r["waste"], settle_ms=r["settle_ms"])
+    for key in ("parity", "cpu_baseline"):
+        if key in r:
+            out[key] = r[key]
+    return out
+
+
+def log_result(r):
+    log(f"[bench]   {r['ms_per_step']:.4f} ms/step  kernel {r['kernel_ms']:.4f} ms  "
+        f"{r['kernel_live_tflops']:.1f} live TFLOP/s (mfma {100 * r['mfma']['frac']:.1f}%, "
+        f"hbm {100 * r['hbm']['frac']:.1f}% of algorithmic bytes; {r['bound']}-bound)  waste {r['waste']}")
+    if r.get("parity"):
+        pr = r["parity"]
+        log(f"[bench]   parity: max {pr['max_abs']:.2e} mean {pr['mean_abs']:.2e} over {pr['rows']} rows x "
+            f"{pr['heads']} heads ({'ok' if pr['within_tolerance'] else 'OUT OF TOLERANCE'})")
+    if r.get("isolated"):
+        log(f"[bench]   isolated {r['isolated']['ms_median']:.4f} ms ({r['isolated']['live_tflops']:.1f} TFLOP/s)")
+    if r.get("index_build"):
+        ib = r["index_build"]
+        log(f"[bench]   index build: device {ib['gpu_ms']:.2f} ms, host C builder {ib['cpu_ms']:.1f} ms "
+            f"on {ib['cpu_threads']} threads ({ib['speedup']:.0f}x)")
+    if r.get("decode"):
+        dd = r["decode"]
+        log("[bench]   decode (append + attend, 1 token): " + ", ".join(
+            f"{b} {dd[b]['ms_per_token'] * 1e3:.1f} us ({dd[b]['gb_per_s']:.0f} GB/s)"
+            for b in dd if isinstance(dd[b], dict)))
+    if r.get("backward"):
+        bw = r["backward"]
+        sb = bw["single_basis"]
+        log(f"[bench]   backward ({' + '.join(bw['pieces'])}, 64x64, {bw['tiles']} tiles): {bw['ms']:.3f} ms, "
+            f"{bw['live_tflops']:.0f} live TFLOP/s ({100 * bw['roofline']['frac']:.1f}%); one pass in "
+            f"{sb['basis']} ({sb['tiles']} tiles): {sb['ms']:.3f} ms")
+    if r.get("permute"):
+        pm_ = r["permute"]
+        log(f"[bench]   permute rp{pm_['residue']}: Q/K/V gather {pm_['gather_qkv']['gb_per_s']:.0f} GB/s, "
+            f"O scatter {pm_['scatter_o']['gb_per_s']:.0f} GB/s")
+
+
+# the other workloads of the default run: (workload, decomposition variant or None)
+CONFIGS = [("window128-L1k", None), ("dilated8-L8k", None), ("dilated8-L8k", "identity"),
+           ("sinkwin-L32k", None), ("prefixlat-L64k", None)]
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # (the untimed warmup also lets the GPU's clocks settle: over the first ~100 ms of load
-    # they are still rising, and a short warmup times that ramp)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--settle-ms", type=float, default=500.0,
+                    help="wall time of back-to-back forwards before the warmup and the timed steps")
     ap.add_argument("--workload", default=None)
     ap.add_argument("--variant", default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="only the headline workload")
     ap.add_argument("--all", action="store_true")
     ap.add_argument("--report", default=None)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -428,31 +589,8 @@ def main():
             for variant in [None] + list(wl.variants):
                 log(f"[bench] {name} {variant or ''}")
                 rows.append(run(name, a.steps, a.warmup, with_cpu=not a.no_cpu and variant is None,
-                                variant=variant))
-                r = rows[-1]
-                log(f"[bench]   {r['ms_per_step']:.4f} ms/step  kernel {r['kernel_ms']:.4f} ms  "
-                    f"{r['kernel_live_tflops']:.1f} live TFLOP/s ({100 * r['frac_peak']:.1f}% of {r['peak_tflops']})"
-                    f"  waste {r['waste']}  isolated {r['isolated']['ms_median']:.4f} ms "
-                    f"({r['isolated']['live_tflops']:.1f} TFLOP/s)")
-                if r.get("index_build"):
-                    ib = r["index_build"]
-                    log(f"[bench]   index build: device {ib['gpu_ms']:.2f} ms, host C builder {ib['cpu_ms']:.1f} ms "
-                        f"on {ib['cpu_threads']} threads ({ib['speedup']:.0f}x)")
-                if r.get("decode"):
-                    dd = r["decode"]
-                    log("[bench]   decode (append + attend, 1 token): " + ", ".join(
-                        f"{b} {dd[b]['ms_per_token'] * 1e3:.1f} us ({dd[b]['gb_per_s']:.0f} GB/s)"
-                        for b in dd if isinstance(dd[b], dict)))
-                if r.get("backward"):
-                    bw = r["backward"]
-                    sb = bw["single_basis"]
-                    log(f"[bench]   backward ({' + '.join(bw['pieces'])}, 64x64, {bw['tiles']} tiles): {bw['ms']:.3f} ms, "
-                        f"{bw['live_tflops']:.0f} live TFLOP/s ({100 * bw['roofline']['frac']:.1f}%); one pass in "
-                        f"{sb['basis']} ({sb['tiles']} tiles): {sb['ms']:.3f} ms")
-                if r.get("permute"):
-                    pm_ = r["permute"]
-                    log(f"[bench]   permute rp{pm_['residue']}: Q/K/V gather {pm_['gather_qkv']['gb_per_s']:.0f} GB/s, "
-                        f"O scatter {pm_['scatter_o']['gb_per_s']:.0f} GB/s")
+                                variant=variant, settle_ms=a.settle_ms))
+                log_result(rows[-1])
         out = dict(device=torch.cuda.get_device_name(0), results=rows)
         if a.report:
             with open(a.report, "w") as f:
@@ -461,8 +599,20 @@ def main():
         return
 
     name = a.workload or workloads.HEADLINE
-    r = run(name, a.steps, a.warmup, with_cpu=not a.no_cpu, variant=a.variant)
+    log(f"[bench] {name} {a.variant or ''}")
+    r = run(name, a.steps, a.warmup, with_cpu=not a.no_cpu, variant=a.variant, settle_ms=a.settle_ms)
+    log_result(r)
+    configs = []
+    if not a.no_configs and a.workload is None:
+        for cname, variant in CONFIGS:
+            log(f"[bench] {cname} {variant or ''}")
+            rc = run(cname, a.steps, a.warmup, with_cpu=not a.no_cpu, variant=variant, extras=False,
+                     settle_ms=min(a.settle_ms, 300.0), cpu_budget=3.0)
+            log_result(rc)
+            configs.append(brief(rc))
     wl = workloads.make(name)
+    traffic, traffic_src = _measured_traffic(r["workload"])
+    main_roof = r["mfma"] if r["bound"] == "mfma" else r["hbm"]
     line = dict(
         metric=METRIC, value=r["live_tflops"], unit="TFLOP/s", n_gpus=1, steps=a.steps, warmup=a.warmup,
         ms_per_step=r["ms_per_step"], higher_is_better=True, scaling="weak", vs_baseline=None,
@@ -471,14 +621,21 @@ def main():
                     live_pairs_per_head=r["live_pairs_per_head"], waste=r["waste"],
                     pct_bf16_peak=round(100 * r["live_tflops"] / PEAK_TFLOPS["bf16"], 2),
                     pieces=r["pieces"], index_build_ms=r["index_build_ms"]),
-        roofline=dict(bound="mfma", achieved=r["kernel_live_tflops"], peak=r["peak_tflops"], unit="TFLOP/s",
-                      frac=r["frac_peak"], traffic=_measured_traffic(r["workload"]),
+        settle_ms=r["settle_ms"],
+        roofline=dict(bound=r["bound"], achieved=main_roof["achieved"], peak=main_roof["peak"],
+                      unit=main_roof["unit"], frac=main_roof["frac"], traffic=traffic,
+                      traffic_unit="HBM bytes per step (all launches of one step)", traffic_source=traffic_src,
+                      intensity_flop_per_byte=r["intensity_flop_per_byte"],
+                      ridge_flop_per_byte=r["ridge_flop_per_byte"], mfma=r["mfma"], hbm=r["hbm"],
                       kernel=" + ".join(sorted({p["kernel"] for p in r["pieces"] if p["kernel"]})) +
-                             " (all launches of one step)",
-                      algorithmic="live FLOP = 4 * D * live pairs * heads per launch"),
+                             " (all launches of one step, durations from HIP events on the launch stream)",
+                      algorithmic="live FLOP = 4 * D * live pairs * heads; algorithmic bytes = Q, K, V read "
+                                  "and O, LSE written once per launch, plus the merge input of a second piece"),
+        parity=r.get("parity"),
         cpu_baseline=r.get("cpu_baseline"),
+        configs=configs,
         index_build=r.get("index_build"),
-        isolated=r["isolated"],
+        isolated=r.get("isolated"),
         permute=r["permute"],
         decode=r["decode"],
         backward=r["backward"],

@@ -112,14 +112,14 @@ class BackwardPlan:
         if N != self.N:
             raise ValueError(f"plan built for N={self.N}, got N={N}")
         ts = (q, k, v, o, do)
+        if lse.dtype != torch.float32 or lse.shape != (BH, N) or lse.stride(1) != 1 or lse.stride(0) < N:
+            raise ValueError("lse must be float32 [BH, N] with unit column stride and row stride >= N")
         _lib.require_device(*ts, lse)
         for t in ts:
             if t.shape != q.shape or t.dtype != q.dtype or t.stride() != q.stride():
                 raise ValueError("q, k, v, o and do must share shape, dtype and strides")
         if q.stride(2) != 1:
             raise ValueError("the last dimension must have unit stride")
-        if lse.dtype != torch.float32 or lse.shape != (BH, N) or lse.stride(1) != 1:
-            raise ValueError("lse must be float32 [BH, N] with unit row stride")
         outs = []
         for t, name in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
             t = torch.empty_like(q) if t is None else t
@@ -131,7 +131,8 @@ class BackwardPlan:
         if dvec is None:
             if dvec_given:
                 raise ValueError("dvec_given needs dvec")
-            dvec = torch.empty((BH, N), dtype=torch.float32, device=q.device)
+            # the kernels index dvec with lse's row stride: give it lse's layout
+            dvec = torch.empty_strided(lse.shape, lse.stride(), dtype=torch.float32, device=q.device)
         elif dvec.dtype != torch.float32 or dvec.shape != (BH, N) or dvec.stride() != lse.stride():
             raise ValueError("dvec must be float32 [BH, N] with lse's strides")
         a = _lib.PaAttnBwdArgs()

@@ -1054,6 +1054,8 @@ extern "C" int pa_attn_bwd(const pa_attn_bwd_args* x, void* stream) {
   PA_CHECK_ARG(x->kv_num && x->q_num && (x->pitch == 0 || (x->kv_idx && x->kv_partial)) &&
                    (x->tpitch == 0 || (x->q_idx && x->q_partial)),
                "pa_attn_bwd: null index array");
+  PA_CHECK_ARG(x->lse_sb >= x->N, "pa_attn_bwd: lse_sb=%lld < N=%lld (lse and dvec rows must not overlap)",
+               (long long)x->lse_sb, (long long)x->N);
   PA_CHECK_ARG(x->sn >= x->D && x->sb >= x->sn && x->sn < (1ll << 28), "pa_attn_bwd: strides sb=%lld sn=%lld",
                (long long)x->sb, (long long)x->sn);
   PA_CHECK_ARG((x->N / 64) * x->BH < (1ll << 31), "pa_attn_bwd: %lld blocks x %lld heads exceed one launch",
@@ -1077,7 +1079,7 @@ extern "C" int pa_attn_bwd(const pa_attn_bwd_args* x, void* stream) {
   k.sn = x->sn;
   k.lse = x->lse;
   k.dvec = x->dvec;
-  k.lse_sb = x->lse_sb > 0 ? x->lse_sb : x->N;
+  k.lse_sb = x->lse_sb;
   k.N = (int32_t)x->N;
   k.nb = (int32_t)(x->N / 64);
   k.scale = x->scale > 0.f ? x->scale : 1.f / sqrtf((float)x->D);

@@ -385,7 +385,8 @@ Plan plan_of(int64_t BH, int64_t capacity, int64_t length, int32_t residue_s) {
   chunk = ((chunk + 255) / 256) * 256;
   if (chunk < 256) chunk = 256;
   // the merge holds one weight per split in LDS
-  while (p.s * ((cnt_max + chunk - 1) / chunk) > kMergeMax) chunk *= 2;
+  // (terminates: s <= kMergeMax is checked, and one chunk per class fits once chunk >= cnt_max)
+  while (chunk < cnt_max && p.s * ((cnt_max + chunk - 1) / chunk) > kMergeMax) chunk *= 2;
   p.chunk = chunk;
   p.per_class = (int32_t)(cnt_max > 0 ? (cnt_max + chunk - 1) / chunk : 0);
   p.n_split = p.s * p.per_class;
@@ -400,6 +401,8 @@ int check_decode(const pa_decode_args* x) {
   PA_CHECK_ARG(x->D == 128 || x->D == 64, "pa_decode: D=%d (64 or 128)", x->D);
   PA_CHECK_ARG(x->dtype != PA_F32 || x->D == 64, "pa_decode: float32 needs D = 64");
   const int32_t s = x->residue_s > 1 ? x->residue_s : 1;
+  // the merge holds one weight per split and every class is at least one split
+  PA_CHECK_ARG(s <= kMergeMax, "pa_decode: residue_s=%d exceeds %d classes", s, kMergeMax);
   PA_CHECK_ARG(x->capacity >= 1 && x->capacity < (1ll << 31) && x->capacity % s == 0,
                "pa_decode: capacity=%lld must be in 1..2^31-1 and a multiple of s=%d", (long long)x->capacity, s);
   PA_CHECK_ARG(x->length >= 0 && x->length <= x->capacity, "pa_decode: length=%lld outside 0..capacity",
@@ -505,6 +508,7 @@ extern "C" int pa_kv_append(const void* k_new, const void* v_new, int64_t new_sb
                             int32_t dtype, int64_t capacity, int64_t pos0, int32_t residue_s, void* stream) {
   PA_CHECK_ARG(dtype == PA_BF16 || dtype == PA_F16 || dtype == PA_F32, "pa_kv_append: dtype %d", dtype);
   const int64_t s = residue_s > 1 ? residue_s : 1;
+  PA_CHECK_ARG(s <= pa::kMergeMax, "pa_kv_append: residue_s=%d exceeds %d classes", residue_s, pa::kMergeMax);
   PA_CHECK_ARG(BH >= 1 && n >= 0 && D >= 1, "pa_kv_append: BH=%lld n=%lld D=%d", (long long)BH, (long long)n, D);
   PA_CHECK_ARG(capacity >= 1 && capacity % s == 0, "pa_kv_append: capacity=%lld not a multiple of s=%lld",
                (long long)capacity, (long long)s);

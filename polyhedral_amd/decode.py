@@ -47,11 +47,17 @@ class DecodeLaunch:
         return self.out
 
 
+# the decode merge holds one weight per split, and every residue class is one split at least
+MAX_CLASSES = 4096
+
+
 class KVCache:
     """Keys and values of BH heads, capacity rows each, in the residue-``residue`` basis."""
 
     def __init__(self, BH, capacity, D, dtype=torch.bfloat16, residue=0, device=None):
         s = int(residue) if residue and residue > 1 else 1
+        if s > MAX_CLASSES:
+            raise ValueError(f"residue={residue}: the decode merge takes at most {MAX_CLASSES} classes")
         if capacity < 1 or capacity % s:
             raise ValueError(f"capacity={capacity} must be a positive multiple of the residue stride {s}")
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())

@@ -1,3 +1,5 @@
 """Counterpart of the reference's polyattn package for the attention hot path:
-``masks`` (the predicate zoo) and ``cost`` (the element-count model) only."""
-from . import cost, masks  # noqa: F401
+``masks`` (the predicate zoo), ``cost`` (the element-count model) and, of
+``transforms``, the per-tile key-row count ``kv_per_tile`` that the traffic driver
+imports."""
+from . import cost, masks, transforms  # noqa: F401

@@ -119,6 +119,7 @@ def test_backward_argument_checks_run_before_any_launch():
               "q_idx", "q_num", "q_partial"):
         setattr(a, f, p)
     a.dtype, a.D, a.BH, a.N, a.sb, a.sn, a.pitch, a.tpitch = _lib.PA_BF16, 128, 2, 1024, 1024 * 128, 128, 4, 4
+    a.lse_sb = 1024
     a.mask.n_include = 1
     a.kv_bits = p                                                           # one of four bitmap arrays
     assert lib.pa_attn_bwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
@@ -144,3 +145,58 @@ def test_backward_argument_checks_run_before_any_launch():
     assert b"q_bits_off" in lib.pa_last_error()
     assert lib.pa_index_bits_transpose(None, 16, 4, p, p, None) == _lib.PA_E_INVALID
     assert lib.pa_index_bits_transpose(p, 16, 0, None, None, None) == _lib.PA_OK   # nothing listed
+
+
+def test_backward_rejects_lse_rows_shorter_than_n():
+    """lse and dvec rows of stride lse_sb < N would overlap (an expanded lse has stride 0)."""
+    lib = _lib.lib()
+    a = _lib.PaAttnBwdArgs()
+    buf = (ctypes.c_int64 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    for f in ("q", "k", "v", "o", "dout", "dq", "dk", "dv", "lse", "dvec", "kv_idx", "kv_num", "kv_partial",
+              "q_idx", "q_num", "q_partial"):
+        setattr(a, f, p)
+    a.dtype, a.D, a.BH, a.N, a.sb, a.sn, a.pitch, a.tpitch = _lib.PA_BF16, 128, 2, 1024, 1024 * 128, 128, 4, 4
+    a.mask.n_include = 1
+    for sb in (0, 512, 1023):
+        a.lse_sb = sb
+        assert lib.pa_attn_bwd(ctypes.byref(a), None) == _lib.PA_E_INVALID
+        assert b"lse_sb" in lib.pa_last_error()
+
+
+def test_backward_host_checks_on_lse_layout():
+    """The Python layer gives dvec lse's strides and refuses an lse whose rows overlap."""
+    import torch
+
+    from polyhedral_amd import backward as pbwd
+    plan = pbwd.BackwardPlan.__new__(pbwd.BackwardPlan)
+    plan.N = 64
+    q = torch.zeros(2, 64, 128, dtype=torch.bfloat16)
+    for lse in (torch.zeros(1, 64).expand(2, 64),     # row stride 0
+                torch.zeros(2, 32)):                  # rows shorter than N
+        with pytest.raises(ValueError, match="lse must be"):
+            plan.backward(q, q, q, q, lse, q)
+
+
+def test_decode_rejects_more_residue_classes_than_the_merge_takes():
+    """residue_s > 4096 left the split planner without an exit; it is an argument error."""
+    lib = _lib.lib()
+    a = _lib.PaDecodeArgs()
+    buf = (ctypes.c_int64 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    a.q, a.k_cache, a.v_cache, a.o = p, p, p, p
+    a.nq, a.BH, a.D, a.dtype = 1, 1, 128, _lib.PA_BF16
+    a.q_sb, a.q_sn, a.c_sb, a.c_sn, a.o_sb, a.o_sn = 128, 128, 16384 * 128, 128, 128, 128
+    a.capacity, a.length, a.residue_s = 16384, 100, 8192
+    a.mask.n_include = 1
+    n = ctypes.c_int64(0)
+    assert lib.pa_decode_workspace(ctypes.byref(a), ctypes.byref(n)) == _lib.PA_E_INVALID
+    assert b"residue_s=8192" in lib.pa_last_error()
+    assert lib.pa_kv_append(p, p, 128, 128, p, p, 16384 * 128, 128, 1, 1, 128, _lib.PA_BF16, 16384, 0, 8192,
+                            None) == _lib.PA_E_INVALID
+    assert b"residue_s=8192" in lib.pa_last_error()
+    a.residue_s = 4096                                 # the largest accepted basis plans normally
+    assert lib.pa_decode_workspace(ctypes.byref(a), ctypes.byref(n)) == _lib.PA_OK and n.value > 0
+    from polyhedral_amd import decode as pdec
+    with pytest.raises(ValueError):
+        pdec.KVCache(1, 16384, 128, residue=8192, device="cpu")
