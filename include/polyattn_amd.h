@@ -133,6 +133,18 @@ int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* k
                    int32_t BQ, int32_t A, int32_t residue_s, int32_t residue_qlog2, const int32_t* order,
                    int32_t* steps, int64_t steps_pitch, void* stream);
 
+/* Persistent run rows of the streaming kernel (no counterpart in the reference): the
+ * step descriptors of n_items work items, item i = (batch-head item_bh[i], query block
+ * item_qb[i]), written to run rows item_off[i] .. item_off[i + 1] - 1 (item_off holds
+ * n_items + 1 offsets).  steps is pa_index_steps output for the index in index order
+ * (order NULL), [nq, steps_pitch, 16], in the launch's residue basis.  A row is the
+ * list's step j with its K / V rows offset by item_bh * N (rows of the whole [BH, N]
+ * tensor), word 9 = (1 if j is the item's first step) | (2 if its last) | item_qb << 2
+ * and word 10 = item_bh.  An item whose list is empty must be given one row: it gets a
+ * step with every code 0 (the kernel writes zeros and log-sum-exp -inf for it). */
+int pa_index_run(const int32_t* steps, int64_t steps_pitch, int32_t nq, int64_t N, const int32_t* item_bh,
+                 const int32_t* item_qb, const int32_t* item_off, int32_t n_items, int32_t* run, void* stream);
+
 /* ---- class-A permutation (replaces gpu/permute.py:12-31) -------------------------
  * Row gather dst[b, p, :] = src[b, perm[p], :] (inverse = 0), the index_select of
  * gpu/permute.py:22-24, or row scatter dst[b, perm[p], :] = src[b, p, :] (inverse = 1),
@@ -217,6 +229,18 @@ typedef struct pa_attn_args {
   int32_t gather_scatter;
   const void* wsel;
   int64_t wsel_sb;
+  /* Persistent schedule (no counterpart in the reference: the Triton kernel runs one
+   * program per (query block, head), gpu/triton_attn.py:210).  run_groups > 0: the
+   * streaming kernel runs as run_groups work-groups, group g taking the run rows
+   * run_start[g] .. run_start[g + 1] - 1 of run_steps (pa_index_run output for this
+   * index, basis and BH) one after the other as a single stream of steps, so no step
+   * pipeline drains between query blocks.  Same preconditions as kv_steps (which is then
+   * not read), plus: the residue basis in closed form for any gather / scatter, q, k, v
+   * and o with batch stride N * row stride, and BH * N * row bytes below 2^32.  Results
+   * are those of the per-block launch. */
+  const int32_t* run_steps;
+  const int32_t* run_start;   /* [run_groups + 1] */
+  int32_t run_groups;
 } pa_attn_args;
 
 int pa_attn_fwd(const pa_attn_args* args, void* stream);

@@ -71,7 +71,7 @@ class Launch:
 
     def __init__(self, args, keep, out, device, kernel):
         self.args, self.keep, self.out, self.device = args, keep, out, device
-        self.kernel = kernel  # "stream" or "general"
+        self.kernel = kernel  # "run", "stream" or "general"
         self._ref = ctypes.byref(args)
 
     def __call__(self):
@@ -98,11 +98,14 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
             perm_q=None, perm_kv=None, gather_kv=False, gather_mult=1, gather_scatter=True,
             num_warps=4, num_stages=2, *, kv_wave_bits=None, kv_bits=None, gather_q=False, scatter_o=False,
             residue=0, lse=None, prev=None, out=None, qblock_order=None, kv_steps=None, kernel="auto",
-            heads_desc=False, wsel=None):
+            heads_desc=False, wsel=None, run=None):
     """Validate the arguments of block_sparse_attention once and return a Launch.
 
     heads_desc: issue the heads from the last to the first (the results are the same; a
-    pass that follows another over the same tensors then starts where the cache is warm)."""
+    pass that follows another over the same tensors then starts where the cache is warm).
+    run: a schedule.RunSchedule of this index for these heads: the streaming kernel then
+    runs persistently, a fixed set of work-groups each taking its list of (head, query
+    block) items as one stream of steps (same results)."""
     BH, N, D = q.shape
     if perm_kv is None:
         perm_kv = perm_q
@@ -240,6 +243,15 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
                 or kv_steps.shape[2] != 16 or not kv_steps.is_contiguous():
             raise ValueError("kv_steps must be contiguous int32 [N/BQ, steps, 16]")
         args.kv_steps, args.steps_pitch = _lib.ptr(kv_steps), kv_steps.shape[1]
+    use_run = use_stream and run is not None
+    if use_run:
+        if (run.BH, run.N, run.residue_s) != (BH, N, steps_basis):
+            raise ValueError(f"run schedule built for BH={run.BH}, N={run.N}, residue {run.residue_s}; "
+                             f"this call has BH={BH}, N={N}, residue {steps_basis}")
+        for t, n in ((k, "k"), (v, "v")):
+            if t.stride(0) != N * t.stride(1):
+                raise ValueError(f"the persistent kernel needs {n} with batch stride N * row stride")
+        args.run_steps, args.run_start, args.run_groups = _lib.ptr(run.run), _lib.ptr(run.start), run.groups
     args.heads_desc = 1 if heads_desc else 0
     wsel_t = None
     if gather_mult > 1:
@@ -255,5 +267,5 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
         args.gather_mult, args.gather_scatter = gather_mult, 1 if gather_scatter else 0
         args.wsel, args.wsel_sb = _lib.ptr(wsel_t), wsel_t.stride(0)
     keep = [q, k, v, o, kv_idx, kv_num, kv_partial, kv_wave_bits, kv_bits, dmask, lse, prev, qblock_order,
-            kv_steps, wsel_t]
-    return Launch(args, keep, o, dev, "stream" if use_stream else "general")
+            kv_steps, wsel_t, run]
+    return Launch(args, keep, o, dev, "run" if use_run else "stream" if use_stream else "general")

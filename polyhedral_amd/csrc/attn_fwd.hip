@@ -9,6 +9,7 @@ int launch_attn_bf16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f32(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s);
+int launch_attn_run(const AttnK& a, int groups, int dtype, hipStream_t s);
 }  // namespace pa
 
 extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
@@ -114,8 +115,28 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   PA_CHECK_ARG(a.total_wg <= 0x7fffffffll, "pa_attn_fwd: %lld work-groups exceed the grid limit",
                (long long)a.total_wg);
 
+  a.run_steps = x->run_steps;
+  a.run_start = x->run_start;
   const int NW = x->BQ >= 32 ? x->BQ / 32 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x->run_groups > 0) {
+    // the persistent streaming kernel: asked for by passing a schedule
+    PA_CHECK_ARG(x->dtype == PA_BF16 || x->dtype == PA_F16, "pa_attn_fwd: run_groups needs f16 or bf16");
+    PA_CHECK_ARG(x->D == 128 && x->BQ == 128 && (x->A == 16 || x->A == 32 || x->A == 64),
+                 "pa_attn_fwd: run_groups needs D = 128, BQ = 128, A in 16, 32, 64 (got D=%d, %dx%d)", x->D, x->BQ,
+                 x->A);
+    PA_CHECK_ARG(x->run_steps && x->run_start, "pa_attn_fwd: run_groups needs run_steps and run_start");
+    PA_CHECK_ARG((reinterpret_cast<uintptr_t>(x->run_steps) & 15) == 0, "pa_attn_fwd: run_steps not 16-byte aligned");
+    PA_CHECK_ARG(x->pitch == 0 || x->kv_bits, "pa_attn_fwd: run_groups needs the partial-tile bitmaps");
+    PA_CHECK_ARG(x->gather_mult <= 1, "pa_attn_fwd: gather_mult > 1 runs on the general kernel");
+    PA_CHECK_ARG(!(x->gather_q || x->scatter_o || x->gather_kv) || x->residue_s > 0,
+                 "pa_attn_fwd: run_groups gathers and scatters through the closed-form residue basis only");
+    PA_CHECK_ARG(x->k_sb == x->N * x->k_sn && x->v_sb == x->N * x->v_sn,
+                 "pa_attn_fwd: run_groups needs k and v with batch stride N * row stride");
+    const int64_t rb = (x->k_sn > x->v_sn ? x->k_sn : x->v_sn) * 2;
+    PA_CHECK_ARG(x->BH * x->N * rb < (1ll << 32), "pa_attn_fwd: BH * N * row bytes too large for run_groups");
+    return pa::launch_attn_run(a, x->run_groups, x->dtype, s);
+  }
   if (x->kv_steps) {
     // the streaming kernel: asked for by passing the step descriptors, so its
     // preconditions are errors rather than a silent change of kernel

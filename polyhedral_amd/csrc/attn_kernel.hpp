@@ -81,6 +81,8 @@ struct AttnK {
   int32_t gather_mult, gather_scatter;  // class-B traffic emulation (K only)
   const char* wsel;
   int64_t wsel_sb;
+  const int32_t* run_steps;  // persistent schedule (attn_run_kernel only): run rows
+  const int32_t* run_start;  //   and each work-group's first row, [groups + 1]
 };
 
 constexpr int kStep = 64;          // KV rows per staged step

@@ -1,22 +1,40 @@
-// Instantiations and launch of the streaming attention kernel (f16, bf16; D = 128, BQ = 128).
-#include "attn_stream.hpp"
+// Instantiations and launches of the streaming attention kernels (f16, bf16; D = 128,
+// BQ = 128): one work-group per (query block, head), or a persistent run of items per
+// work-group.
+#include "attn_run.hpp"
 
 namespace pa {
 
-template <typename T>
-static int launch_stream_t(const AttnK& a, hipStream_t s, const char* name) {
+template <typename K>
+static int raise_lds_limit(K kernel, unsigned long long& configured, const char* what) {
   // the dynamic LDS limit is raised once per device
-  static unsigned long long configured = 0ull;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (dev >= 64 || !((configured >> dev) & 1ull)) {
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_stream_kernel<T>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kStreamSmem);
-    if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(attn_stream_kernel)");
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kStreamSmem);
+    if (e != hipSuccess) return hip_fail(e, what);
     if (dev < 64) configured |= 1ull << dev;
   }
+  return PA_OK;
+}
+
+template <typename T>
+static int launch_stream_t(const AttnK& a, hipStream_t s, const char* name) {
+  static unsigned long long configured = 0ull;
+  if (int rc = raise_lds_limit(&attn_stream_kernel<T>, configured, "hipFuncSetAttribute(attn_stream_kernel)"))
+    return rc;
   hipLaunchKernelGGL(attn_stream_kernel<T>, dim3((unsigned)a.total_wg), dim3(256), kStreamSmem, s, a);
+  PA_LAUNCH_CHECK(name);
+  return PA_OK;
+}
+
+template <typename T>
+static int launch_run_t(const AttnK& a, int groups, hipStream_t s, const char* name) {
+  static unsigned long long configured = 0ull;
+  if (int rc = raise_lds_limit(&attn_run_kernel<T>, configured, "hipFuncSetAttribute(attn_run_kernel)")) return rc;
+  hipLaunchKernelGGL(attn_run_kernel<T>, dim3((unsigned)groups), dim3(256), kStreamSmem, s, a);
   PA_LAUNCH_CHECK(name);
   return PA_OK;
 }
@@ -24,6 +42,11 @@ static int launch_stream_t(const AttnK& a, hipStream_t s, const char* name) {
 int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s) {
   if (dtype == PA_BF16) return launch_stream_t<__bf16>(a, s, "attn_stream_kernel<bf16>");
   return launch_stream_t<_Float16>(a, s, "attn_stream_kernel<f16>");
+}
+
+int launch_attn_run(const AttnK& a, int groups, int dtype, hipStream_t s) {
+  if (dtype == PA_BF16) return launch_run_t<__bf16>(a, groups, s, "attn_run_kernel<bf16>");
+  return launch_run_t<_Float16>(a, groups, s, "attn_run_kernel<f16>");
 }
 
 }  // namespace pa

@@ -204,36 +204,7 @@ void attn_stream_kernel(const AttnK a) {
                  ((cw >> 1) & 1u) | ((cw >> 8) & 2u) | ((cw >> 15) & 4u) | ((cw >> 22) & 8u)};
   };
 
-  // DMA of a step's K rows and bitmaps (slot SL of the K ring and of the bitmap slots)
-  // and of its V rows (slot SL of the V ring).  The descriptor holds each segment's K / V
-  // row already mapped through the gather basis; a past-the-list segment loads row 0
-  // (valid memory) and has code 0, so its scores are -inf and its P is 0.
-#define PA_SEG_ROW(dd, t) ((dd).base[t])
-#define PA_DMA_K(dd, SL)                                                                          \
-  do {                                                                                            \
-    _Pragma("unroll") for (int t = 0; t < 4; ++t)                                                 \
-      dma_x4(lds0 + kKring + (SL) * kSlot + (16 * t + 4 * w) * 256,                               \
-             kbase + (uint32_t)PA_SEG_ROW(dd, t) * krow_b32, k_goff);                             \
-    if (A >= 32) {                                                                                \
-      const int lbw = w >> 1;                                                                     \
-      const int off = lbw == 0 ? (dd).boff[0] : (dd).boff[2];                                     \
-      if (off >= 0)                                                                               \
-        dma_x1(lds0 + kBits + (SL) * kBitsSlot + lbw * 1024 + (w & 1) * 256, bits + (int64_t)off * 4, \
-               b_goff);                                                                           \
-    } else {                                                                                      \
-      const int off = w == 0 ? (dd).boff[0] : w == 1 ? (dd).boff[1] : w == 2 ? (dd).boff[2] : (dd).boff[3]; \
-      if (off >= 0) {                                                                             \
-        dma_x1(lds0 + kBits + (SL) * kBitsSlot + w * 512, bits + (int64_t)off * 4, b_goff);       \
-        dma_x1(lds0 + kBits + (SL) * kBitsSlot + w * 512 + 256, bits + (int64_t)off * 4, b_goff + 256); \
-      }                                                                                           \
-    }                                                                                             \
-  } while (0)
-#define PA_DMA_V(dd, SL)                                                                          \
-  do {                                                                                            \
-    _Pragma("unroll") for (int t = 0; t < 4; ++t)                                                 \
-      dma_x4(lds0 + kVring + (SL) * kSlot + (16 * t + 4 * w) * 256,                               \
-             vbase + (uint32_t)PA_SEG_ROW(dd, t) * vrow_b32, v_goff);                             \
-  } while (0)
+#include "attn_stream_ops.inc"
 
   // DMA of rows 64 h .. 64 h + 63 of the previous partial into K slot SL.
 #define PA_DMA_PREV(h, SL)                                                                        \
@@ -242,138 +213,6 @@ void attn_stream_kernel(const AttnK a) {
       const int r_ = qb * 128 + 64 * (h) + 16 * t;                                                \
       const int pr_ = prev_closed ? (r_ & rmask) * a.residue_s + (r_ >> a.residue_qlog2) : r_;    \
       dma_x4(lds0 + kKring + (SL) * kSlot + (16 * t + 4 * w) * 256, pbase + (int64_t)pr_ * a.prev_sn * 2, p_goff); \
-    }                                                                                             \
-  } while (0)
-
-  // QK of both blocks of the step in K slot SL: 4 K reads ahead, then one read per MFMA
-  // (the order is spelled out for the scheduler: left alone it trades the overlap for
-  // registers and waits on every read).
-#define PA_QK(S0, S1, SL)                                                                         \
-  do {                                                                                            \
-    u32x4 ka[NQF], kb[NQF];                                                                       \
-    _Pragma("unroll") for (int kc = 0; kc < NQF; ++kc) ka[kc] = *(lds_u4*)(kptr[kc] + (SL) * kSlot); \
-    _Pragma("unroll") for (int kc = 0; kc < NQF; ++kc) kb[kc] = *(lds_u4*)(kptr[kc] + (SL) * kSlot + 8192); \
-    S0 = Mma<T>::mma(__builtin_bit_cast(Frag, ka[0]), qf[0], f32x16{0});                           \
-    _Pragma("unroll") for (int kc = 1; kc < NQF; ++kc)                                            \
-      S0 = Mma<T>::mma(__builtin_bit_cast(Frag, ka[kc]), qf[kc], S0);                              \
-    S1 = Mma<T>::mma(__builtin_bit_cast(Frag, kb[0]), qf[0], f32x16{0});                           \
-    _Pragma("unroll") for (int kc = 1; kc < NQF; ++kc)                                            \
-      S1 = Mma<T>::mma(__builtin_bit_cast(Frag, kb[kc]), qf[kc], S1);                              \
-  } while (0)
-#define PA_QK_ORDER()                                                                             \
-  do {                                                                                            \
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);                                            \
-    _Pragma("unroll") for (int q_ = 0; q_ < 2 * NQF - 4; ++q_) {                                  \
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                          \
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                          \
-    }                                                                                             \
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                            \
-  } while (0)
-
-  // Mask block lb of S (some pairs dead for this wave) from bitmap slot BS: bit c of the
-  // lane's row word is kv column c of the block; element i of S is column 8 (i / 4) +
-  // 4 G + i % 4.
-#define PA_MASK(S, BS, lb, fl)                                                                    \
-  do {                                                                                            \
-    uint32_t word;                                                                                \
-    if (A >= 32) {                                                                                \
-      word = *(lds_u32*)(bptr + (BS) * kBitsSlot + (lb) * 1024);                                  \
-    } else {                                                                                      \
-      const uint32_t t0 = 2 * (lb), t1 = 2 * (lb) + 1;                                            \
-      const uint32_t lo = ((fl).full >> t0) & 1u ? 0xffffu                                        \
-                          : ((fl).live >> t0) & 1u ? *(lds_u32*)(bptr + (BS) * kBitsSlot + t0 * 512) & 0xffffu \
-                                                   : 0u;                                          \
-      const uint32_t hi = ((fl).full >> t1) & 1u ? 0xffffu                                        \
-                          : ((fl).live >> t1) & 1u ? *(lds_u32*)(bptr + (BS) * kBitsSlot + t1 * 512) & 0xffffu \
-                                                   : 0u;                                          \
-      word = lo | (hi << 16);                                                                     \
-    }                                                                                             \
-    word >>= 4 * G;                                                                               \
-    _Pragma("unroll") for (int i = 0; i < 16; ++i) {                                              \
-      /* (a scalar copy: bit-casting the vector element itself reads element 0) */               \
-      const float sv = S[i];                                                                      \
-      const int32_t keep = __builtin_amdgcn_sbfe((int32_t)word, 8 * (i >> 2) + (i & 3), 1);       \
-      S[i] = __builtin_bit_cast(float, (__builtin_bit_cast(int32_t, sv) & keep) |                 \
-                                           (int32_t)(0xff800000u & ~(uint32_t)keep));             \
-    }                                                                                             \
-  } while (0)
-
-  // Bring block lb of freshly computed scores to what the softmax may see: -inf for a
-  // block dead for this wave, masked for a partial one, unchanged when full.
-#define PA_SHAPE(S, BS, lb, fl)                                                                   \
-  do {                                                                                            \
-    const uint32_t bm = 3u << (2 * (lb));                                                         \
-    if (!((fl).live & bm)) {                                                                      \
-      _Pragma("unroll") for (int i = 0; i < 16; ++i) S[i] = -INFINITY;                            \
-    } else if (((fl).full & bm) != bm) {                                                          \
-      PA_MASK(S, BS, lb, fl);                                                                     \
-    }                                                                                             \
-  } while (0)
-
-  // Row maximum over the live blocks of the next step, raised into m_run lazily (after
-  // that step's predecessor has been accumulated at the old maximum).
-#define PA_BLOCK_MAX(mx, S)                                                                       \
-  _Pragma("unroll") for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(S[i], S[i + 1]))
-#define PA_RAISE(mx)                                                                              \
-  do {                                                                                            \
-    const float m_new = fmaxf(m_run, row_max(mx) * cexp);                                         \
-    if (__ballot(m_new > m_run + kLazy) != 0ull) {                                                \
-      const float alpha = exp2f(m_run - m_new);                                                   \
-      m_run = m_new;                                                                              \
-      l_part *= alpha;                                                                            \
-      _Pragma("unroll") for (int i = 0; i < NDB; ++i) acc[i] *= alpha;                            \
-    }                                                                                             \
-  } while (0)
-
-  // P of chunk c (16 kv rows) of block S: exp2(S c - m), packed, summed into l_part.
-#define PA_EXP(PF, S, c)                                                                          \
-  do {                                                                                            \
-    f32x8 pv;                                                                                     \
-    _Pragma("unroll") for (int e = 0; e < 8; ++e)                                                 \
-      pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[8 * (c) + e], cexp, neg_m));                 \
-    PF = Mma<T>::cvt(pv);                                                                         \
-    const uint4 pw = __builtin_bit_cast(uint4, PF);                                               \
-    l_part = dot2_sum<T>(pw.x, l_part);                                                           \
-    l_part = dot2_sum<T>(pw.y, l_part);                                                           \
-    l_part = dot2_sum<T>(pw.z, l_part);                                                           \
-    l_part = dot2_sum<T>(pw.w, l_part);                                                           \
-  } while (0)
-  // P.V of chunk c of block lb from V slot SL.
-#define PA_PV(PF, SL, lb, c)                                                                      \
-  do {                                                                                            \
-    _Pragma("unroll") for (int db = 0; db < NDB; ++db) {                                          \
-      lds_cptr v1 = vptr[db] + (SL) * kSlot + (32 * (lb) + 16 * (c)) * 256;                       \
-      const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(v1));                  \
-      const s16x4 x2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(v1 + 8 * 256));        \
-      const uint4 vx = {__builtin_bit_cast(uint2, x1).x, __builtin_bit_cast(uint2, x1).y,         \
-                        __builtin_bit_cast(uint2, x2).x, __builtin_bit_cast(uint2, x2).y};        \
-      acc[db] = Mma<T>::mma(__builtin_bit_cast(Frag, vx), PF, acc[db]);                            \
-    }                                                                                             \
-  } while (0)
-
-  // Order of the straight-line iteration, spelled out for the scheduler: 4 K reads
-  // ahead; 16 x (QK MFMA, LDS read, 6 VALU of the exponentials); 4 more reads, so the
-  // transposed V reads run 4 MFMAs ahead; 12 x (P.V MFMA, 2 reads, 1 VALU); 4 x (P.V
-  // MFMA, 1 VALU).  Each MFMA then runs while the
-  // wave issues the VALU work of the other half of the pipeline, and the fragments in
-  // flight stay few enough for two waves per SIMD.
-#define PA_FAST_ORDER()                                                                           \
-  do {                                                                                            \
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);                                            \
-    _Pragma("unroll") for (int q_ = 0; q_ < 2 * NQF; ++q_) {                                      \
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                                          \
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);                                          \
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);                                          \
-    }                                                                                             \
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);                                            \
-    _Pragma("unroll") for (int q_ = 0; q_ < 4 * NDB - 4; ++q_) {                                  \
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                                          \
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);                                          \
-      __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);                                          \
-    }                                                                                             \
-    _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                            \
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);                                          \
-      __builtin_amdgcn_sched_group_barrier(0x002, 1, 1);                                          \
     }                                                                                             \
   } while (0)
 

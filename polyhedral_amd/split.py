@@ -29,6 +29,7 @@ from .attention import prepare
 from .index import STREAM_TILES, build_device, build_steps
 from .perm import residue_perm
 from .polyattn.masks import Permuted
+from .schedule import RunSchedule
 from .spec import MaskSpec
 
 
@@ -52,9 +53,13 @@ class SplitPlan:
     create_block_mask), then reused by every forward.  order="lpt" issues each
     piece's query blocks longest first; None keeps index order."""
 
-    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto"):
+    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto", persistent=True):
         self.N = N
         self.kernel = kernel
+        # persistent: run the streaming pieces on the persistent kernel (a fixed set of
+        # work-groups, each a list of items as one stream of steps)
+        self.persistent = persistent and kernel != "general"
+        self._runs = {}
         self.pieces = list(pieces)
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self.device = dev
@@ -77,9 +82,13 @@ class SplitPlan:
             # the streaming kernel's descriptors, laid out in that issue order
             steps = (build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], N, p.BQ, p.A,
                                  _closed_form_residue(p, N), qorder) if stream else None)
+            # the persistent kernel's run rows come from the descriptors in index order
+            runnable = stream and self.persistent and (perm_t is None or _closed_form_residue(p, N) > 0)
+            steps_idx = (build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], N, p.BQ, p.A,
+                                     _closed_form_residue(p, N), None) if runnable else None)
             self.built.append(dict(piece=p, spec=MaskSpec(tuple(inc), tuple(exc)), perm=perm_t,
                                    kv_idx=kv_idx, kv_num=kv_num, kv_partial=kv_partial, wave=wave, bits=bits,
-                                   steps=steps,
+                                   steps=steps, steps_idx=steps_idx,
                                    tiles=tiles, live=live, order=qorder))
 
     @property
@@ -108,16 +117,33 @@ class SplitPlan:
                 # all-empty plan still runs, to write zeros and -inf)
                 continue
             permuted = b["perm"] is not None
+            run = self._run_for(bi_, BH, keep_empty=first) if self._runnable(q, k, v, b) else None
             launches.append(prepare(
                 q, k, v, b["kv_idx"], b["kv_num"], b["kv_partial"], b["spec"], 0, 0, 0, p.BQ, p.A,
                 scale=scale, perm_q=b["perm"], perm_kv=b["perm"], gather_kv=permuted,
                 kv_wave_bits=b["wave"], kv_bits=b["bits"], gather_q=permuted, scatter_o=permuted,
                 residue=_closed_form_residue(p, N),
                 lse=lse_buf, prev=None if first else (o, lse_buf), out=o, qblock_order=b["order"],
-                kv_steps=b["steps"], kernel=self.kernel, heads_desc=len(launches) % 2 == 1))
+                kv_steps=b["steps"], kernel=self.kernel, heads_desc=len(launches) % 2 == 1, run=run))
             self.launched.append(bi_)
             first = False
         return launches, o, lse_buf
+
+    def _runnable(self, q, k, v, b):
+        """Whether the persistent kernel takes this piece over these tensors."""
+        if b.get("steps_idx") is None:
+            return False
+        BH, N, D = q.shape
+        return (q.dtype in (torch.float16, torch.bfloat16) and D == 128 and
+                all(t.stride(0) == N * t.stride(1) for t in (k, v)) and
+                BH * N * max(k.stride(1), v.stride(1)) * 2 < 2 ** 32)
+
+    def _run_for(self, i, BH, keep_empty):
+        key = (i, BH, keep_empty)
+        if key not in self._runs:
+            b = self.built[i]
+            self._runs[key] = RunSchedule(b["steps_idx"], self.N, BH, keep_empty=keep_empty)
+        return self._runs[key]
 
     def forward(self, q, k, v, scale=None, out=None, lse=None):
         """o [BH, N, D] in q's dtype; lse (float32 [BH, N]) receives the merged log-sum-exp."""
