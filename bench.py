@@ -385,9 +385,13 @@ def algorithmic_bytes(plan, wl, esz):
     t = wl.H * wl.L * wl.D * esz
     lse = wl.H * wl.L * 4
     out = []
-    for i, _ in enumerate(plan.launched):
-        rd = 3 * t + (t + lse if i > 0 else 0)
+    first = True
+    for pieces in plan.launched:
+        # one launch runs one piece, or both pieces of a split (Q, K, V read and O, LSE
+        # written once; the merge input stays on chip or in cache)
+        rd = 3 * t + (t + lse if not first else 0)
         out.append(dict(read=rd, write=t + lse))
+        first = False
     return out
 
 
@@ -443,11 +447,18 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0", extra
         torch.cuda.synchronize()
     backward = (measure_backward(wl, q, k, v, o, lse, max(residues) if residues else 0)
                 if extras and wl.D in (64, 128) and wl.dtype != torch.float32 and wl.L % 64 == 0 else None)
-    kernels = [{"run": "attn_run_kernel", "stream": "attn_stream_kernel"}.get(x.kernel, "attn_fwd_kernel")
-               for x in launches]
+    kernels = [{"run": "attn_run_kernel", "split": "attn_run_kernel (split)",
+                "stream": "attn_stream_kernel"}.get(x.kernel, "attn_fwd_kernel") for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
-    for i, bi in enumerate(plan.launched):
-        per[bi] = per_launch[i]
+    piece_kernel = [None] * len(plan.built)
+    for i, pcs in enumerate(plan.launched):
+        for bi in pcs:
+            # a launch of several pieces is attributed to them by live pairs
+            share = plan.built[bi]["live"] / max(1, sum(plan.built[x]["live"] for x in pcs))
+            per[bi] = per_launch[i] * share
+            piece_kernel[bi] = kernels[i]
+    if hasattr(plan, "check"):
+        plan.check()
     live = plan.live
     flops_live = 4 * wl.D * live * wl.H
     flops_tile = 4 * wl.D * plan.elements * wl.H
@@ -464,7 +475,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0", extra
         waste=round(plan.elements / live, 4) if live else None,
         pieces=[dict(mask=b["piece"].mask.name, BQ=b["piece"].BQ, A=b["piece"].A,
                      basis="identity" if b["perm"] is None else "permuted", tiles=b["tiles"], live=b["live"],
-                     kernel=kernels[plan.launched.index(i)] if i in plan.launched else None,
+                     kernel=piece_kernel[i],
                      launch_ms=round(per[i], 5),
                      live_tflops=round(4 * wl.D * b["live"] * wl.H / (per[i] * 1e-3) / 1e12, 2) if per[i] else None)
                 for i, b in enumerate(plan.built)],

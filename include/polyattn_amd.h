@@ -134,16 +134,21 @@ int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* k
                    int32_t* steps, int64_t steps_pitch, void* stream);
 
 /* Persistent run rows of the streaming kernel (no counterpart in the reference): the
- * step descriptors of n_items work items, item i = (batch-head item_bh[i], query block
- * item_qb[i]), written to run rows item_off[i] .. item_off[i + 1] - 1 (item_off holds
- * n_items + 1 offsets).  steps is pa_index_steps output for the index in index order
- * (order NULL), [nq, steps_pitch, 16], in the launch's residue basis.  A row is the
- * list's step j with its K / V rows offset by item_bh * N (rows of the whole [BH, N]
- * tensor), word 9 = (1 if j is the item's first step) | (2 if its last) | item_qb << 2
- * and word 10 = item_bh.  An item whose list is empty must be given one row: it gets a
- * step with every code 0 (the kernel writes zeros and log-sum-exp -inf for it). */
-int pa_index_run(const int32_t* steps, int64_t steps_pitch, int32_t nq, int64_t N, const int32_t* item_bh,
-                 const int32_t* item_qb, const int32_t* item_off, int32_t n_items, int32_t* run, void* stream);
+ * step descriptors of n_items work items, item i = (piece item_piece[i], batch-head
+ * item_bh[i], query block item_qb[i], sync group item_sync[i]), written to run rows
+ * item_off[i] .. item_off[i + 1] - 1 (item_off holds n_items + 1 offsets).  steps[p] is
+ * pa_index_steps output for piece p's index in index order (order NULL), [nq,
+ * steps_pitch[p], 16], in that piece's residue basis; n_pieces is 1 or 2 (item_piece and
+ * item_sync may be NULL: piece 0, no sync group).  A row is the list's step j with its K /
+ * V rows offset by item_bh * N (rows of the whole [BH, N] tensor), its bitmap offsets
+ * (those >= 0) by boff_base[p] (the piece's part of one shared pool; NULL: 0), word 9 =
+ * (1 if j is the item's first step) | (2 if its last) | (4 for piece 1) | item_qb << 3,
+ * word 10 = item_bh and word 11 = item_sync (-1: none).  An item whose list is empty must
+ * be given one row: it gets a step with every code 0 (the kernel writes zeros and
+ * log-sum-exp -inf for it, or leaves a merged row as it was). */
+int pa_index_run(const int32_t* const* steps, const int64_t* steps_pitch, const int32_t* boff_base, int32_t n_pieces,
+                 int64_t N, const int32_t* item_piece, const int32_t* item_bh, const int32_t* item_qb,
+                 const int32_t* item_sync, const int32_t* item_off, int32_t n_items, int32_t* run, void* stream);
 
 /* ---- class-A permutation (replaces gpu/permute.py:12-31) -------------------------
  * Row gather dst[b, p, :] = src[b, perm[p], :] (inverse = 0), the index_select of
@@ -244,6 +249,38 @@ typedef struct pa_attn_args {
 } pa_attn_args;
 
 int pa_attn_fwd(const pa_attn_args* args, void* stream);
+
+/* A two-piece disjoint split in ONE persistent launch (no counterpart in the reference,
+ * which prices a split, src/polyattn/experiments/compose.py:107-119, but has no code for
+ * it).  `first` and `second` are the arguments each piece would take as a run launch of
+ * its own (run_groups > 0, the split's run rows): the first writes o and lse, the second
+ * merges into them in place (prev_o = first->o, prev_lse = first->lse), over the same
+ * q, k, v, o, lse, shapes, dtype, scale and tile; they may differ in basis (residue_s,
+ * gather / scatter flags) and index.  The run rows (pa_index_run, two pieces) carry both
+ * pieces' items and each item's sync group: the rows of a second-piece item are covered
+ * by `sync_signal` first-piece items of its group, and a group has `sync_wait`
+ * second-piece items.  kv_bits is both pieces' bitmaps in one pool (the rows' offsets
+ * point into it).  sync is int32 [2 * sync_groups], all zero before the first launch;
+ * every launch leaves it zero again.  The launch is cooperative (PA_E_INVALID if the
+ * run's work-groups cannot all be resident at once).  *status (int32) is set to 1 if a
+ * merge gave up waiting for its group (the results are then invalid; zero it again, and
+ * sync, before reuse).  The schedule must list every second-piece item after the
+ * first-piece items of its group in each work-group's order. */
+typedef struct pa_split_args {
+  const pa_attn_args* first;
+  const pa_attn_args* second;
+  const int32_t* run_steps;
+  const int32_t* run_start;   /* [run_groups + 1] */
+  int32_t run_groups;
+  const uint32_t* kv_bits;
+  int32_t* sync;
+  int32_t sync_groups;
+  int32_t sync_signal;
+  int32_t sync_wait;
+  int32_t* status;
+} pa_split_args;
+
+int pa_attn_fwd_split(const pa_split_args* args, void* stream);
 
 /* ---- log-sum-exp merge of a disjoint split (spec: src/polyattn/experiments/compose.py:7-17)
  * o[b, r, :] = sum_k exp(lse_k - M) o_k / sum_k exp(lse_k - M), M = max_k lse_k;

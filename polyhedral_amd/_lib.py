@@ -14,7 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libpolyattn_amd.s
 PA_OK, PA_E_INVALID, PA_E_HIP, PA_E_UNSUPPORTED = 0, -1, -2, -3
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 MAX_TERMS = 8
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -43,6 +43,13 @@ class PaAttnArgs(ctypes.Structure):
                 ("prev_lse", c_vp), ("qblock_order", c_vp), ("kv_steps", c_vp), ("steps_pitch", c_i64),
                 ("heads_desc", c_i32), ("gather_mult", c_i32), ("gather_scatter", c_i32), ("wsel", c_vp),
                 ("wsel_sb", c_i64), ("run_steps", c_vp), ("run_start", c_vp), ("run_groups", c_i32)]
+
+
+class PaSplitArgs(ctypes.Structure):
+    _fields_ = [("first", ctypes.POINTER(PaAttnArgs)), ("second", ctypes.POINTER(PaAttnArgs)),
+                ("run_steps", c_vp), ("run_start", c_vp), ("run_groups", c_i32), ("kv_bits", c_vp),
+                ("sync", c_vp), ("sync_groups", c_i32), ("sync_signal", c_i32), ("sync_wait", c_i32),
+                ("status", c_vp)]
 
 
 class PaDecodeArgs(ctypes.Structure):
@@ -75,7 +82,9 @@ SIGNATURES = {
                                      c_vp, c_vp, c_vp]),
     "pa_index_steps": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp,
                                       c_vp, c_i64, c_vp]),
-    "pa_index_run": (ctypes.c_int, [c_vp, c_i64, c_i32, c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp]),
+    "pa_index_run": (ctypes.c_int, [ctypes.POINTER(c_vp), ctypes.POINTER(c_i64), ctypes.POINTER(c_i32), c_i32, c_i64,
+                                    c_vp, c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp]),
+    "pa_attn_fwd_split": (ctypes.c_int, [ctypes.POINTER(PaSplitArgs), c_vp]),
     "pa_permute_rows": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                        c_i32, c_vp]),
     "pa_permute_stack": (ctypes.c_int, [c_vp, c_vp, c_i32, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,

@@ -103,9 +103,9 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
 
     heads_desc: issue the heads from the last to the first (the results are the same; a
     pass that follows another over the same tensors then starts where the cache is warm).
-    run: a schedule.RunSchedule of this index for these heads: the streaming kernel then
-    runs persistently, a fixed set of work-groups each taking its list of (head, query
-    block) items as one stream of steps (same results)."""
+    run: a schedule.RunSchedule of this index for these heads (or (schedule, piece)): the
+    streaming kernel then runs persistently, a fixed set of work-groups each taking its
+    list of (head, query block) items as one stream of steps (same results)."""
     BH, N, D = q.shape
     if perm_kv is None:
         perm_kv = perm_q
@@ -245,8 +245,10 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
         args.kv_steps, args.steps_pitch = _lib.ptr(kv_steps), kv_steps.shape[1]
     use_run = use_stream and run is not None
     if use_run:
-        if (run.BH, run.N, run.residue_s) != (BH, N, steps_basis):
-            raise ValueError(f"run schedule built for BH={run.BH}, N={run.N}, residue {run.residue_s}; "
+        # run = (schedule, the piece of its rows this call is)
+        run, piece = run if isinstance(run, tuple) else (run, 0)
+        if (run.BH, run.N, run.residues[piece]) != (BH, N, steps_basis):
+            raise ValueError(f"run schedule built for BH={run.BH}, N={run.N}, residue {run.residues[piece]}; "
                              f"this call has BH={BH}, N={N}, residue {steps_basis}")
         for t, n in ((k, "k"), (v, "v")):
             if t.stride(0) != N * t.stride(1):

@@ -9,10 +9,12 @@ int launch_attn_bf16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f32(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s);
-int launch_attn_run(const AttnK& a, int groups, int dtype, hipStream_t s);
+int launch_attn_run(const AttnK& a, int groups, int dtype, bool cooperative, hipStream_t s);
 }  // namespace pa
 
-extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
+namespace pa {
+// Checks every argument of one launch and fills the kernel arguments (no launch).
+static int fill_attn(const pa_attn_args* x, AttnK& a) {
   PA_CHECK_ARG(x != nullptr, "pa_attn_fwd: null args");
   PA_CHECK_ARG(x->q && x->k && x->v && x->o, "pa_attn_fwd: null q/k/v/o");
   PA_CHECK_ARG(x->kv_num, "pa_attn_fwd: null kv_num");
@@ -52,7 +54,7 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
                "pa_attn_fwd: prev_dtype %d", x->prev_dtype);
   PA_CHECK_ARG(!x->prev_o || x->lse_sb >= x->N, "pa_attn_fwd: lse_sb=%lld < N", (long long)x->lse_sb);
   PA_CHECK_ARG(!x->lse || x->lse_sb >= x->N, "pa_attn_fwd: lse_sb=%lld < N", (long long)x->lse_sb);
-  if (int rc = pa::check_mask(&x->mask, x->N)) return rc;
+  if (int rc = check_mask(&x->mask, x->N)) return rc;
   // 16-B vector access of every row start
   const int esz = x->dtype == PA_F32 ? 4 : 2;
   auto al = [&](const void* p, int64_t sb, int64_t sn) {
@@ -62,7 +64,7 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
                    al(x->o, x->o_sb, x->o_sn),
                "pa_attn_fwd: q/k/v/o rows must be 16-byte aligned");
 
-  pa::AttnK a;
+  a = AttnK{};
   a.q = static_cast<const char*>(x->q);
   a.k = static_cast<const char*>(x->k);
   a.v = static_cast<const char*>(x->v);
@@ -85,7 +87,7 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   a.pitch = x->pitch;
   a.kv_bits_off = x->kv_bits_off;
   a.kv_bits = x->kv_bits;
-  a.pred = pa::make_pred(x->mask);
+  a.pred = make_pred(x->mask);
   a.gather_q = x->gather_q;
   a.gather_kv = x->gather_kv;
   a.scatter_o = x->scatter_o;
@@ -117,8 +119,10 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
 
   a.run_steps = x->run_steps;
   a.run_start = x->run_start;
-  const int NW = x->BQ >= 32 ? x->BQ / 32 : 1;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  a.run_res[0] = a.residue_s;
+  a.run_qlog2[0] = a.residue_qlog2;
+  a.run_flags[0] = (x->gather_q ? kPieceGatherQ : 0) | (x->gather_kv ? kPieceGatherKV : 0) |
+                   (x->scatter_o ? kPieceScatterO : 0) | (x->prev_o ? kPieceMerge : 0);
   if (x->run_groups > 0) {
     // the persistent streaming kernel: asked for by passing a schedule
     PA_CHECK_ARG(x->dtype == PA_BF16 || x->dtype == PA_F16, "pa_attn_fwd: run_groups needs f16 or bf16");
@@ -135,8 +139,17 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
                  "pa_attn_fwd: run_groups needs k and v with batch stride N * row stride");
     const int64_t rb = (x->k_sn > x->v_sn ? x->k_sn : x->v_sn) * 2;
     PA_CHECK_ARG(x->BH * x->N * rb < (1ll << 32), "pa_attn_fwd: BH * N * row bytes too large for run_groups");
-    return pa::launch_attn_run(a, x->run_groups, x->dtype, s);
   }
+  return PA_OK;
+}
+}  // namespace pa
+
+extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
+  pa::AttnK a;
+  if (int rc = pa::fill_attn(x, a)) return rc;
+  const int NW = x->BQ >= 32 ? x->BQ / 32 : 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x->run_groups > 0) return pa::launch_attn_run(a, x->run_groups, x->dtype, false, s);
   if (x->kv_steps) {
     // the streaming kernel: asked for by passing the step descriptors, so its
     // preconditions are errors rather than a silent change of kernel
@@ -165,4 +178,46 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
     case PA_F16: return pa::launch_attn_f16(a, x->D, NW, s);
     default: return pa::launch_attn_f32(a, x->D, NW, s);
   }
+}
+
+extern "C" int pa_attn_fwd_split(const pa_split_args* x, void* stream) {
+  PA_CHECK_ARG(x && x->first && x->second, "pa_attn_fwd_split: null arguments");
+  const pa_attn_args* f = x->first;
+  const pa_attn_args* g = x->second;
+  pa::AttnK a, b;
+  if (int rc = pa::fill_attn(f, a)) return rc;
+  if (int rc = pa::fill_attn(g, b)) return rc;
+  PA_CHECK_ARG(f->run_groups > 0 && g->run_groups == f->run_groups && x->run_groups == f->run_groups &&
+                   f->run_steps == x->run_steps && g->run_steps == x->run_steps && f->run_start == x->run_start &&
+                   g->run_start == x->run_start,
+               "pa_attn_fwd_split: both pieces must be run launches over the split's run rows");
+  PA_CHECK_ARG(f->q == g->q && f->k == g->k && f->v == g->v && f->o == g->o && f->lse == g->lse &&
+                   f->q_sb == g->q_sb && f->q_sn == g->q_sn && f->k_sb == g->k_sb && f->k_sn == g->k_sn &&
+                   f->v_sb == g->v_sb && f->v_sn == g->v_sn && f->o_sb == g->o_sb && f->o_sn == g->o_sn &&
+                   f->lse_sb == g->lse_sb && f->BH == g->BH && f->N == g->N && f->D == g->D &&
+                   f->dtype == g->dtype && f->scale == g->scale && f->BQ == g->BQ && f->A == g->A,
+               "pa_attn_fwd_split: the pieces differ in tensors, shapes, dtype, scale or tile");
+  PA_CHECK_ARG(f->lse && !f->prev_o, "pa_attn_fwd_split: the first piece writes o and lse (no prev_o)");
+  PA_CHECK_ARG(g->prev_o == f->o && g->prev_lse == f->lse && g->prev_dtype == f->dtype && g->prev_sb == f->o_sb &&
+                   g->prev_sn == f->o_sn,
+               "pa_attn_fwd_split: the second piece merges into the first piece's o and lse");
+  PA_CHECK_ARG(x->kv_bits || (f->pitch == 0 && g->pitch == 0), "pa_attn_fwd_split: null kv_bits");
+  PA_CHECK_ARG(x->sync && x->status && x->sync_groups >= 1 && x->sync_signal >= 1 && x->sync_wait >= 1,
+               "pa_attn_fwd_split: sync=%p status=%p groups=%d signal=%d wait=%d", (void*)x->sync,
+               (void*)x->status, x->sync_groups, x->sync_signal, x->sync_wait);
+  a.kv_bits = x->kv_bits;
+  a.run_res[1] = b.run_res[0];
+  a.run_qlog2[1] = b.run_qlog2[0];
+  a.run_flags[1] = b.run_flags[0];
+  a.prev_o = b.prev_o;
+  a.prev_dtype = b.prev_dtype;
+  a.prev_sb = b.prev_sb;
+  a.prev_sn = b.prev_sn;
+  a.prev_lse = b.prev_lse;
+  a.run_sync = x->sync;
+  a.run_sync_groups = x->sync_groups;
+  a.run_sync_signal = x->sync_signal;
+  a.run_sync_wait = x->sync_wait;
+  a.run_status = x->status;
+  return pa::launch_attn_run(a, x->run_groups, f->dtype, true, static_cast<hipStream_t>(stream));
 }

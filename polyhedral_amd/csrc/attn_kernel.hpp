@@ -83,7 +83,17 @@ struct AttnK {
   int64_t wsel_sb;
   const int32_t* run_steps;  // persistent schedule (attn_run_kernel only): run rows
   const int32_t* run_start;  //   and each work-group's first row, [groups + 1]
+  // attn_run_kernel: the pieces a run's rows may name (word 9 bit 2), each with its own
+  // basis and role, and the counters of a two-piece split in one launch
+  int32_t run_res[2], run_qlog2[2];  // closed-form residue basis of piece p (0: none)
+  int32_t run_flags[2];              // piece p: gather_q 1, gather_kv 2, scatter_o 4, merge 8
+  int32_t* run_sync;                 // [2 * run_sync_groups]: items finished, merges done
+  int32_t run_sync_groups, run_sync_signal, run_sync_wait;
+  int32_t* run_status;               // set to 1 when a merge gives up waiting
 };
+
+// flags of a piece of a persistent run (AttnK::run_flags)
+constexpr int kPieceGatherQ = 1, kPieceGatherKV = 2, kPieceScatterO = 4, kPieceMerge = 8;
 
 constexpr int kStep = 64;          // KV rows per staged step
 constexpr float kSentinel = -1e30f;

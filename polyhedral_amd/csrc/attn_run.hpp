@@ -5,9 +5,9 @@
 // is not one (query block, head) item: it is one of a fixed number of work-groups (two
 // per CU) and runs a precomputed list of items back to back as ONE stream of steps
 // (pa_index_run).  Each run row is a step descriptor that also names its item (head,
-// query block) and whether it is the item's first or last step, with its K / V rows
-// given as rows of the whole [BH, N] tensor.  So the software pipeline never drains
-// between items:
+// query block, piece) and whether it is the item's first or last step, with its K / V
+// rows given as rows of the whole [BH, N] tensor.  So the software pipeline never
+// drains between items:
 //
 //  * the DMA of the next item's first K / V tiles is issued while the current item's
 //    last steps run, exactly as for any other step two iterations ahead;
@@ -16,19 +16,37 @@
 //  * the current item's epilogue (row sum, log-sum-exp, merge with a previous partial,
 //    output store) runs after its last P.V, beside the next item's first scores.
 //
-// What a separate work-group per item pays at its start (kernel arguments, the first
-// descriptor, Q and the first K / V tiles from memory, all exposed, while the other
-// work-group on the CU starts at the same moment) is paid once per work-group here.
+// A run may hold the items of two pieces of a disjoint split (a band in the identity
+// basis and a lattice in a residue basis, say), so that one launch computes the whole
+// forward and the second piece finds the first piece's output, its query rows and much
+// of its K / V in the L2 / memory-side cache instead of re-reading them from HBM.  An
+// item of the second piece merges into the rows the first piece wrote, so it waits for
+// them: the rows of a query block of one piece are covered by `run_sync_signal` query
+// blocks of the other (one sync group), the first piece's items publish their rows and
+// count themselves in the group, and the second piece's items wait for the count before
+// their epilogue reads those rows.  The published rows are written and read with
+// agent-scope (sc1) accesses and the count with agent-scope atomics, so the handshake
+// holds whichever XCD the two items run on.  The schedule orders every item after the
+// items it waits for in each work-group's list, and the launch is cooperative (every
+// work-group resident), so every wait ends; a wait is also bounded, and one that gives
+// up sets *run_status for the host to report.  The last waiter of a group resets both
+// of its counters, so they are zero again for the next launch.
 #pragma once
 
 #include "attn_stream.hpp"
 
 namespace pa {
 
-// word 9 of a run row: bit 0 = the item's first step, bit 1 = its last step, the item's
-// query block in the bits above; word 10: the item's batch-head
+// word 9 of a run row: bit 0 = the item's first step, bit 1 = its last step, bit 2 = the
+// piece, the item's query block in the bits above; word 10: the item's batch-head;
+// word 11: the item's sync group (-1: none)
 constexpr int kRunFirst = 1;
 constexpr int kRunLast = 2;
+constexpr int kRunPiece = 4;
+constexpr int kRunQbShift = 3;
+// polls of a sync counter before a merge gives up (each poll sleeps ~0.4 us); once one
+// merge has given up (*run_status set), the others stop waiting at once
+constexpr int kRunMaxPolls = 1 << 20;
 
 template <typename T>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -55,11 +73,6 @@ void attn_run_kernel(const AttnK a) {
   const StepDesc* desc = reinterpret_cast<const StepDesc*>(a.run_steps) + s_begin;
   const int A = a.A;
 
-  const bool closed = a.residue_s != 0;
-  const int32_t rmask = (1 << a.residue_qlog2) - 1;
-  const bool gather_kv = a.gather_kv && closed;
-  const int rstride = gather_kv ? a.residue_s : 1;
-
   // run rows hold K / V rows of the whole tensor (head offset included; 32-bit byte
   // offsets, checked on the host)
   const char* kbase = a.k;
@@ -68,11 +81,16 @@ void attn_run_kernel(const AttnK a) {
   const char* bits = reinterpret_cast<const char*>(a.kv_bits);
   const int wpr = (A + 31) >> 5;
 
-  // ---- DMA geometry (loop invariant; as attn_stream_kernel) ---------------------
+  // ---- DMA geometry (loop invariant; as attn_stream_kernel, for each piece's basis:
+  // a gathered piece's 16-row segment is 16 rows s apart in memory) -------------------
   const int rs = 4 * w + (lane >> 4);
   const int pu = lane & 15;
-  const uint32_t k_goff = (uint32_t)(rs * rstride) * krow_b32 + 16u * (uint32_t)(pu ^ rs);
-  const uint32_t v_goff = (uint32_t)(rs * rstride) * vrow_b32 + 16u * (uint32_t)(pu ^ (4 * (rs & 3)));
+  const int rstr0 = (a.run_flags[0] & kPieceGatherKV) ? a.run_res[0] : 1;
+  const int rstr1 = (a.run_flags[1] & kPieceGatherKV) ? a.run_res[1] : 1;
+  const uint32_t k_goff0 = (uint32_t)(rs * rstr0) * krow_b32 + 16u * (uint32_t)(pu ^ rs);
+  const uint32_t v_goff0 = (uint32_t)(rs * rstr0) * vrow_b32 + 16u * (uint32_t)(pu ^ (4 * (rs & 3)));
+  const uint32_t k_goff1 = (uint32_t)(rs * rstr1) * krow_b32 + 16u * (uint32_t)(pu ^ rs);
+  const uint32_t v_goff1 = (uint32_t)(rs * rstr1) * vrow_b32 + 16u * (uint32_t)(pu ^ (4 * (rs & 3)));
   const uint32_t b_goff = A >= 32 ? (uint32_t)((64 * (w & 1) + lane) * wpr * 4) : (uint32_t)(lane * 4);
 
   // ---- LDS read geometry ---------------------------------------------------------
@@ -95,16 +113,17 @@ void attn_run_kernel(const AttnK a) {
   lds_cptr bptr = lds + kBits + (w * 32 + m) * 4;
   asm volatile("" : "+v"(bptr));
 
-  // index-space query row of this lane in query block qb, and its row in the tensors
-  auto q_orig_of = [&](int r_idx) __attribute__((always_inline)) -> int {
-    return closed ? (r_idx & rmask) * a.residue_s + (r_idx >> a.residue_qlog2) : r_idx;
+  // original row of index-space row r_idx in piece pc's basis
+  auto q_orig_of = [&](int pc, int r_idx) __attribute__((always_inline)) -> int {
+    const int s = a.run_res[pc];
+    return s ? (r_idx & ((1 << a.run_qlog2[pc]) - 1)) * s + (r_idx >> a.run_qlog2[pc]) : r_idx;
   };
 
-  // ---- Q fragments (B operand of S^T = K Q^T) of item (bh, qb) --------------------
+  // ---- Q fragments (B operand of S^T = K Q^T) of item (bh, qb) of piece pc ---------
   Frag qf[NQF];
-  auto load_q = [&](int bh, int qb) __attribute__((always_inline)) {
+  auto load_q = [&](int pc, int bh, int qb) __attribute__((always_inline)) {
     const int r_idx = qb * 128 + w * 32 + m;
-    const int r_load = a.gather_q ? q_orig_of(r_idx) : r_idx;
+    const int r_load = (a.run_flags[pc] & kPieceGatherQ) ? q_orig_of(pc, r_idx) : r_idx;
     const char* qrow = a.q + ((int64_t)bh * a.q_sb + (int64_t)r_load * a.q_sn) * ESZ;
 #pragma unroll
     for (int kc = 0; kc < NQF; ++kc)
@@ -130,8 +149,9 @@ void attn_run_kernel(const AttnK a) {
     r.boff[1] = c[6];
     r.boff[2] = c[7];
     r.boff[3] = c[8];
-    r.pad[0] = c[9];   // flags | qb << 2
+    r.pad[0] = c[9];   // flags | piece | qb << 3
     r.pad[1] = c[10];  // bh
+    r.pad[2] = c[11];  // sync group
     return r;
   };
   struct Flags {
@@ -145,30 +165,58 @@ void attn_run_kernel(const AttnK a) {
 
 #include "attn_stream_ops.inc"
 
-  // ---- epilogue of item (bh, qb): normalise, merge with the previous partial, store ----
-  // Every previous-partial element is loaded before the first store (the output may be
-  // the previous partial itself: the merge is in place, each lane rewriting what it read).
+  // ---- epilogue of item (bh, qb) of piece pc: normalise, merge with the previous
+  // partial, store; in a split run, publish the rows (first piece) or wait for them
+  // (second piece).  Every previous-partial element is loaded before the first store
+  // (the output may be the previous partial itself: the merge is in place, each lane
+  // rewriting what it read).  Row pointers include the lane's column offset 4 G, so every
+  // column below is an immediate offset: no per-column address stays live across items.
   const bool prev16 = a.prev_o && a.prev_dtype != PA_F32;
-  auto finish = [&](int bh, int qb) __attribute__((always_inline)) {
+  auto finish = [&](int pc, int bh, int qb, int sg) __attribute__((always_inline)) {
+    const int flags = a.run_flags[pc];
+    const bool merge = (flags & kPieceMerge) != 0;
+    const bool signal = a.run_sync && sg >= 0 && !merge;   // publishes rows another piece merges into
+    const bool waits = a.run_sync && sg >= 0 && merge;     // merges into rows another item publishes
     const int r_idx = qb * 128 + w * 32 + m;
-    const int srow = a.scatter_o ? q_orig_of(r_idx) : r_idx;
+    const int srow = (flags & kPieceScatterO) ? q_orig_of(pc, r_idx) : r_idx;
     const float l_tot = row_sum(l_part);
     const bool has = l_tot > 0.f;
     float lse_v = has ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
     float a_own = has ? 1.f / l_tot : 0.f;
     float a_prev = 0.f;
-    // (row pointers include the lane's column offset 4 G, so every column below is an
-    // immediate offset: no per-column address stays live across the loop)
+    if (waits) {
+      // every item of the other piece that covers these rows has published them
+      if (tid == 0) {
+        int polls = 0;
+        while (__hip_atomic_load(a.run_sync + sg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a.run_sync_signal) {
+          if (++polls >= kRunMaxPolls) {
+            __hip_atomic_store(a.run_status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          if (__hip_atomic_load(a.run_status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+          __builtin_amdgcn_s_sleep(16);
+        }
+      }
+      __syncthreads();
+    }
     uint2 prevw[NDB * 4];
     const int psz = prev16 ? 2 : 4;
-    const char* prow =
-        a.prev_o ? a.prev_o + ((int64_t)bh * a.prev_sb + (int64_t)srow * a.prev_sn + 4 * G) * psz : nullptr;
-    if (a.prev_o) {
-      const float lp = a.prev_lse[(int64_t)bh * a.lse_sb + srow];
+    const char* prow = merge ? a.prev_o + ((int64_t)bh * a.prev_sb + (int64_t)srow * a.prev_sn + 4 * G) * psz : nullptr;
+    if (merge) {
+      const float* lp_at = a.prev_lse + (int64_t)bh * a.lse_sb + srow;
+      const float lp = waits ? __hip_atomic_load(lp_at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *lp_at;
       if (prev16) {
+        if (waits) {
 #pragma unroll
-        for (int q_ = 0; q_ < NDB * 4; ++q_)
-          prevw[q_] = *reinterpret_cast<const uint2*>(prow + (32 * (q_ >> 2) + 8 * (q_ & 3)) * 2);
+          for (int q_ = 0; q_ < NDB * 4; ++q_)
+            prevw[q_] = __builtin_bit_cast(
+                uint2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(prow + (32 * (q_ >> 2) + 8 * (q_ & 3)) * 2),
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        } else {
+#pragma unroll
+          for (int q_ = 0; q_ < NDB * 4; ++q_)
+            prevw[q_] = *reinterpret_cast<const uint2*>(prow + (32 * (q_ >> 2) + 8 * (q_ & 3)) * 2);
+        }
       }
       const float M = fmaxf(lse_v, lp);
       if (M == -INFINITY) {
@@ -202,10 +250,35 @@ void attn_run_kernel(const AttnK a) {
             x += a_prev * load4_any(prow + d0 * 4, PA_F32);
           }
         }
-        *reinterpret_cast<u32x2*>(orow + d0 * ESZ) = __builtin_bit_cast(u32x2, Mma<T>::cvt4(x));
+        const u32x2 ov = __builtin_bit_cast(u32x2, Mma<T>::cvt4(x));
+        if (signal)
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(orow + d0 * ESZ), __builtin_bit_cast(uint64_t, ov),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          *reinterpret_cast<u32x2*>(orow + d0 * ESZ) = ov;
       }
     }
-    if (a.lse && G == 0) a.lse[(int64_t)bh * a.lse_sb + srow] = lse_v;
+    if (a.lse && G == 0) {
+      float* lo = a.lse + (int64_t)bh * a.lse_sb + srow;
+      if (signal)
+        __hip_atomic_store(lo, lse_v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        *lo = lse_v;
+    }
+    if (signal) {
+      // the rows are complete in memory before the group counts them
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0) __hip_atomic_fetch_add(a.run_sync + sg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (waits && tid == 0) {
+      // the last of the group's merges resets both counters for the next launch
+      const int done = __hip_atomic_fetch_add(a.run_sync + a.run_sync_groups + sg, 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      if (done == a.run_sync_wait - 1) {
+        __hip_atomic_store(a.run_sync + sg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.run_sync + a.run_sync_groups + sg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NDB; ++i) acc[i] = f32x16{0};
     m_run = kSentinel;
@@ -217,14 +290,21 @@ void attn_run_kernel(const AttnK a) {
   // is jj, and the Q rows of the item that starts at jj + 2 when jj + 1 ends an item
   // (QK of jj + 1 was the last use of the fragments).  The uses of the Q fragments right
   // after the wait make the compiler place its own wait for Q there, before this
-  // iteration's DMA is issued (a wait at the QK would also wait for that DMA).
+  // iteration's DMA is issued (a wait at the QK would also wait for that DMA).  Each
+  // step's DMA takes the row offsets of its piece's basis.
 #define PA_RITER(jj, P)                                                                           \
   do {                                                                                            \
     dma_wait_all();                                                                               \
     _Pragma("unroll") for (int kc = 0; kc < NQF; ++kc) asm volatile("" ::"v"(qf[kc]));             \
     __syncthreads();                                                                              \
-    if ((jj) + 2 < n_steps) PA_DMA_K(d_j2, (P));                                                  \
-    PA_DMA_V(d_j1, (P) ^ 1);                                                                      \
+    if ((jj) + 2 < n_steps) {                                                                     \
+      const uint32_t k_goff = (d_j2.pad[0] & kRunPiece) ? k_goff1 : k_goff0;                      \
+      PA_DMA_K(d_j2, (P));                                                                        \
+    }                                                                                             \
+    {                                                                                             \
+      const uint32_t v_goff = (d_j1.pad[0] & kRunPiece) ? v_goff1 : v_goff0;                      \
+      PA_DMA_V(d_j1, (P) ^ 1);                                                                    \
+    }                                                                                             \
     StepDesc d_j3{};                                                                              \
     if ((jj) + 3 < n_steps) d_j3 = load_desc((jj) + 3);                                           \
     const Flags fn = flags_of(d_j1.code);                                                         \
@@ -245,11 +325,13 @@ void attn_run_kernel(const AttnK a) {
       PA_FAST_ORDER();                                                                            \
     }                                                                                             \
     if (fl_c & kRunLast) {                                                                        \
-      finish(cur_bh, cur_qb);                                                                     \
+      finish((fl_c >> 2) & 1, cur_bh, cur_qb, cur_sg);                                            \
       cur_bh = d_j1.pad[1];                                                                       \
-      cur_qb = fl_n >> 2;                                                                         \
+      cur_qb = fl_n >> kRunQbShift;                                                               \
+      cur_sg = d_j1.pad[2];                                                                       \
     }                                                                                             \
-    if ((fl_n & kRunLast) && (jj) + 2 < n_steps) load_q(d_j2.pad[1], d_j2.pad[0] >> 2);           \
+    if ((fl_n & kRunLast) && (jj) + 2 < n_steps)                                                  \
+      load_q((d_j2.pad[0] >> 2) & 1, d_j2.pad[1], d_j2.pad[0] >> kRunQbShift);                    \
     PA_SHAPE(sn0, (P) ^ 1, 0, fn);                                                                \
     PA_SHAPE(sn1, (P) ^ 1, 1, fn);                                                                \
     if (fn.live) {                                                                                \
@@ -290,23 +372,31 @@ void attn_run_kernel(const AttnK a) {
   StepDesc d_j1{}, d_j2{};
   Flags fc{0u, 0u};
   int fl_c;
-  int cur_bh, cur_qb;
+  int cur_bh, cur_qb, cur_sg;
   f32x16 sc0, sc1;
   {
     const StepDesc d0 = load_desc(0);
     if (n_steps > 1) d_j1 = load_desc(1);
     if (n_steps > 2) d_j2 = load_desc(2);
     cur_bh = d0.pad[1];
-    cur_qb = d0.pad[0] >> 2;
+    cur_qb = d0.pad[0] >> kRunQbShift;
+    cur_sg = d0.pad[2];
     fl_c = d0.pad[0];
-    load_q(cur_bh, cur_qb);
-    PA_DMA_K(d0, 0);
-    PA_DMA_V(d0, 0);
+    load_q((fl_c >> 2) & 1, cur_bh, cur_qb);
+    {
+      const uint32_t k_goff = (d0.pad[0] & kRunPiece) ? k_goff1 : k_goff0;
+      const uint32_t v_goff = (d0.pad[0] & kRunPiece) ? v_goff1 : v_goff0;
+      PA_DMA_K(d0, 0);
+      PA_DMA_V(d0, 0);
+    }
     dma_wait_all();
 #pragma unroll
     for (int kc = 0; kc < NQF; ++kc) asm volatile("" ::"v"(qf[kc]));
     __syncthreads();
-    if (n_steps > 1) PA_DMA_K(d_j1, 1);
+    if (n_steps > 1) {
+      const uint32_t k_goff = (d_j1.pad[0] & kRunPiece) ? k_goff1 : k_goff0;
+      PA_DMA_K(d_j1, 1);
+    }
     fc = flags_of(d0.code);
     PA_QK(sc0, sc1, 0);
     PA_QK_ORDER();
@@ -316,7 +406,8 @@ void attn_run_kernel(const AttnK a) {
     PA_BLOCK_MAX(mx, sc0);
     PA_BLOCK_MAX(mx, sc1);
     m_run = fmaxf(m_run, row_max(mx) * cexp);
-    if (n_steps > 1 && (fl_c & kRunLast)) load_q(d_j1.pad[1], d_j1.pad[0] >> 2);
+    if (n_steps > 1 && (fl_c & kRunLast))
+      load_q((d_j1.pad[0] >> 2) & 1, d_j1.pad[1], d_j1.pad[0] >> kRunQbShift);
   }
   // iterations 0 .. n_steps - 2 (two per trip, so every slot offset is a constant)
   int j = 0;
@@ -332,7 +423,7 @@ void attn_run_kernel(const AttnK a) {
     PA_RLAST(1);
   else
     PA_RLAST(0);
-  finish(cur_bh, cur_qb);
+  finish((fl_c >> 2) & 1, cur_bh, cur_qb, cur_sg);
 
 #undef PA_RITER
 #undef PA_RLAST

@@ -381,16 +381,28 @@ extern "C" int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, cons
 namespace pa {
 namespace {
 
-// One work-group of 64 threads per item: its run rows are its list's steps with the K / V
-// rows moved to the item's head and the item written into words 9 and 10.
-__global__ __launch_bounds__(64) void run_kernel(const int32_t* __restrict__ steps, int64_t steps_pitch, int64_t N,
+// One work-group of 64 threads per item: its run rows are its list's steps (from the
+// descriptors of its piece) with the K / V rows moved to the item's head, the bitmap
+// offsets moved to the piece's part of a shared pool, and the item written into words
+// 9 to 11.
+struct RunPieces {
+  const int32_t* steps[2];
+  int64_t pitch[2];
+  int32_t boff_base[2];
+};
+
+__global__ __launch_bounds__(64) void run_kernel(const RunPieces pcs, int64_t N, const int32_t* __restrict__ item_piece,
                                                  const int32_t* __restrict__ item_bh,
                                                  const int32_t* __restrict__ item_qb,
+                                                 const int32_t* __restrict__ item_sync,
                                                  const int32_t* __restrict__ item_off, int32_t* __restrict__ run) {
   const int i = blockIdx.x;
+  const int pc = item_piece ? item_piece[i] : 0;
   const int32_t bh = item_bh[i], qb = item_qb[i];
+  const int32_t sg = item_sync ? item_sync[i] : -1;
   const int32_t r0 = item_off[i], len = item_off[i + 1] - r0;
-  const int32_t* list = steps + (int64_t)qb * steps_pitch * 16;
+  const int32_t* list = (pc ? pcs.steps[1] : pcs.steps[0]) + (int64_t)qb * (pc ? pcs.pitch[1] : pcs.pitch[0]) * 16;
+  const int32_t bbase = pc ? pcs.boff_base[1] : pcs.boff_base[0];
   const int32_t n_list = list[14];  // the list's number of steps (0: an empty list)
   const int32_t head_row = (int32_t)(bh * N);
   for (int j = threadIdx.x; j < len; j += 64) {
@@ -405,6 +417,9 @@ __global__ __launch_bounds__(64) void run_kernel(const int32_t* __restrict__ ste
         d[4 * u + 2] = x.z;
         d[4 * u + 3] = x.w;
       }
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (d[5 + t] >= 0) d[5 + t] += bbase;
     } else {
       // the one step of an empty list: every code 0 (the scores are -inf), rows 0 of the
       // head (valid memory), no bitmaps
@@ -415,8 +430,9 @@ __global__ __launch_bounds__(64) void run_kernel(const int32_t* __restrict__ ste
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) d[t] += head_row;
-    d[9] = (j == 0 ? 1 : 0) | (j == len - 1 ? 2 : 0) | (qb << 2);
+    d[9] = (j == 0 ? 1 : 0) | (j == len - 1 ? 2 : 0) | (pc ? 4 : 0) | (qb << 3);
     d[10] = bh;
+    d[11] = sg;
     int4* dst = reinterpret_cast<int4*>(run + ((int64_t)r0 + j) * 16);
 #pragma unroll
     for (int u = 0; u < 4; ++u) dst[u] = int4{d[4 * u], d[4 * u + 1], d[4 * u + 2], d[4 * u + 3]};
@@ -426,18 +442,28 @@ __global__ __launch_bounds__(64) void run_kernel(const int32_t* __restrict__ ste
 }  // namespace
 }  // namespace pa
 
-extern "C" int pa_index_run(const int32_t* steps, int64_t steps_pitch, int32_t nq, int64_t N, const int32_t* item_bh,
-                            const int32_t* item_qb, const int32_t* item_off, int32_t n_items, int32_t* run,
-                            void* stream) {
+extern "C" int pa_index_run(const int32_t* const* steps, const int64_t* steps_pitch, const int32_t* boff_base,
+                            int32_t n_pieces, int64_t N, const int32_t* item_piece, const int32_t* item_bh,
+                            const int32_t* item_qb, const int32_t* item_sync, const int32_t* item_off, int32_t n_items,
+                            int32_t* run, void* stream) {
   PA_CHECK_ARG(n_items >= 0, "pa_index_run: n_items=%d", n_items);
   if (n_items == 0) return PA_OK;
-  PA_CHECK_ARG(steps && item_bh && item_qb && item_off && run, "pa_index_run: null argument");
-  PA_CHECK_ARG(steps_pitch >= 1 && nq >= 1, "pa_index_run: steps_pitch=%lld nq=%d", (long long)steps_pitch, nq);
+  PA_CHECK_ARG(n_pieces == 1 || n_pieces == 2, "pa_index_run: n_pieces=%d (1 or 2)", n_pieces);
+  PA_CHECK_ARG(steps && steps_pitch && item_bh && item_qb && item_off && run, "pa_index_run: null argument");
+  PA_CHECK_ARG(n_pieces == 1 || item_piece, "pa_index_run: two pieces need item_piece");
   PA_CHECK_ARG(N >= 1 && N <= (1ll << 30), "pa_index_run: N=%lld out of range", (long long)N);
-  PA_CHECK_ARG((reinterpret_cast<uintptr_t>(steps) & 15) == 0 && (reinterpret_cast<uintptr_t>(run) & 15) == 0,
-               "pa_index_run: steps and run must be 16-byte aligned");
-  hipLaunchKernelGGL(pa::run_kernel, dim3((unsigned)n_items), dim3(64), 0, static_cast<hipStream_t>(stream), steps,
-                     steps_pitch, N, item_bh, item_qb, item_off, run);
+  pa::RunPieces pcs{};
+  for (int p = 0; p < n_pieces; ++p) {
+    PA_CHECK_ARG(steps[p] && steps_pitch[p] >= 1, "pa_index_run: piece %d has no descriptors", p);
+    PA_CHECK_ARG((reinterpret_cast<uintptr_t>(steps[p]) & 15) == 0, "pa_index_run: steps not 16-byte aligned");
+    pcs.steps[p] = steps[p];
+    pcs.pitch[p] = steps_pitch[p];
+    pcs.boff_base[p] = boff_base ? boff_base[p] : 0;
+    PA_CHECK_ARG(pcs.boff_base[p] >= 0, "pa_index_run: negative bitmap base");
+  }
+  PA_CHECK_ARG((reinterpret_cast<uintptr_t>(run) & 15) == 0, "pa_index_run: run must be 16-byte aligned");
+  hipLaunchKernelGGL(pa::run_kernel, dim3((unsigned)n_items), dim3(64), 0, static_cast<hipStream_t>(stream), pcs, N,
+                     item_piece, item_bh, item_qb, item_sync, item_off, run);
   PA_LAUNCH_CHECK("run_kernel");
   return PA_OK;
 }

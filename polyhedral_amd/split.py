@@ -18,6 +18,7 @@ through pa_attn_fwd:
 Pieces must be disjoint (the peeling of compose.py:49-76 makes them so); the merge
 of disjoint pieces equals single-pass attention over their union.
 """
+import ctypes
 from dataclasses import dataclass
 from typing import Optional
 
@@ -29,7 +30,7 @@ from .attention import prepare
 from .index import STREAM_TILES, build_device, build_steps
 from .perm import residue_perm
 from .polyattn.masks import Permuted
-from .schedule import RunSchedule
+from .schedule import RunSchedule, SplitSchedule
 from .spec import MaskSpec
 
 
@@ -53,12 +54,17 @@ class SplitPlan:
     create_block_mask), then reused by every forward.  order="lpt" issues each
     piece's query blocks longest first; None keeps index order."""
 
-    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto", persistent=True):
+    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto", persistent=True, fuse=True,
+                 split_xcds=None):
         self.N = N
         self.kernel = kernel
         # persistent: run the streaming pieces on the persistent kernel (a fixed set of
-        # work-groups, each a list of items as one stream of steps)
+        # work-groups, each a list of items as one stream of steps); fuse: a two-piece
+        # split runs as ONE persistent launch, the second piece merging into the first
+        # piece's rows as soon as they are written (pa_attn_fwd_split)
         self.persistent = persistent and kernel != "general"
+        self.fuse = fuse and self.persistent
+        self.split_xcds = split_xcds   # XCD partition of a split launch's schedule (None: all 8)
         self._runs = {}
         self.pieces = list(pieces)
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
@@ -100,15 +106,21 @@ class SplitPlan:
         return sum(b["tiles"] * b["piece"].BQ * b["piece"].A for b in self.built)
 
     def prepare(self, q, k, v, scale=None, out=None, lse=None):
-        """One validated Launch per piece over these tensors; calling them in order is a forward.
-        Returns (launches, o, lse)."""
+        """Validated launches over these tensors; calling them in order is a forward.
+        Returns (launches, o, lse).  self.launched lists, per launch, the pieces it runs
+        (indices into self.built): one piece per launch, or both pieces of a two-piece
+        split in one launch (pa_attn_fwd_split)."""
         BH, N, D = q.shape
         if N != self.N:
             raise ValueError(f"plan built for N={self.N}, got N={N}")
         o = out if out is not None else torch.empty_like(q)
         lse_buf = lse if lse is not None else torch.empty((BH, N), dtype=torch.float32, device=q.device)
+        fused = self._fused_launch(q, k, v, scale, o, lse_buf)
+        if fused is not None:
+            self.launched = [(0, 1)]
+            return [fused], o, lse_buf
         launches = []
-        self.launched = []          # index into self.built of each launch, in order
+        self.launched = []
         first = True
         for bi_, b in enumerate(self.built):
             p = b["piece"]
@@ -125,9 +137,53 @@ class SplitPlan:
                 residue=_closed_form_residue(p, N),
                 lse=lse_buf, prev=None if first else (o, lse_buf), out=o, qblock_order=b["order"],
                 kv_steps=b["steps"], kernel=self.kernel, heads_desc=len(launches) % 2 == 1, run=run))
-            self.launched.append(bi_)
+            self.launched.append((bi_,))
             first = False
         return launches, o, lse_buf
+
+    def _fused_launch(self, q, k, v, scale, o, lse_buf):
+        """The whole forward of a two-piece split as one persistent launch, or None when
+        this plan or these tensors do not allow it (then one launch per piece)."""
+        if not (self.fuse and len(self.built) == 2):
+            return None
+        b0, b1 = self.built
+        if b0["live"] == 0 or b1["live"] == 0 or (b0["piece"].BQ, b1["piece"].BQ) != (128, 128):
+            return None
+        if b0["piece"].A != b1["piece"].A:
+            return None
+        if not (self._runnable(q, k, v, b0) and self._runnable(q, k, v, b1)):
+            return None
+        BH = q.shape[0]
+        key = ("split", BH)
+        if key not in self._runs:
+            pools = [b0["bits"][1], b1["bits"][1]]
+            try:
+                sched = SplitSchedule(b0["steps_idx"], b1["steps_idx"], _closed_form_residue(b0["piece"], self.N),
+                                      _closed_form_residue(b1["piece"], self.N), self.N, BH,
+                                      (0, pools[0].numel()), xcds=self.split_xcds)
+            except ValueError:
+                sched = None
+            self._runs[key] = (sched, torch.cat(pools) if sched is not None else None)
+        sched, pool = self._runs[key]
+        if sched is None:
+            return None
+        ls = []
+        for i, b in enumerate((b0, b1)):
+            p = b["piece"]
+            permuted = b["perm"] is not None
+            ls.append(prepare(
+                q, k, v, b["kv_idx"], b["kv_num"], b["kv_partial"], b["spec"], 0, 0, 0, p.BQ, p.A,
+                scale=scale, perm_q=b["perm"], perm_kv=b["perm"], gather_kv=permuted,
+                kv_wave_bits=b["wave"], kv_bits=b["bits"], gather_q=permuted, scatter_o=permuted,
+                residue=_closed_form_residue(p, self.N), lse=lse_buf, prev=None if i == 0 else (o, lse_buf), out=o,
+                kv_steps=b["steps"], kernel=self.kernel, run=(sched, i)))
+        return SplitLaunch(ls[0], ls[1], sched, pool)
+
+    def check(self):
+        """Raise if a merge of a past split launch gave up waiting (see SplitSchedule.check)."""
+        for key, val in self._runs.items():
+            if key[0] == "split" and val[0] is not None:
+                val[0].check()
 
     def _runnable(self, q, k, v, b):
         """Whether the persistent kernel takes this piece over these tensors."""
@@ -143,7 +199,7 @@ class SplitPlan:
         if key not in self._runs:
             b = self.built[i]
             self._runs[key] = RunSchedule(b["steps_idx"], self.N, BH, keep_empty=keep_empty)
-        return self._runs[key]
+        return (self._runs[key], 0)
 
     def forward(self, q, k, v, scale=None, out=None, lse=None):
         """o [BH, N, D] in q's dtype; lse (float32 [BH, N]) receives the merged log-sum-exp."""
@@ -152,6 +208,31 @@ class SplitPlan:
             for launch in launches:
                 launch()
         return o
+
+
+class SplitLaunch:
+    """Both pieces of a two-piece split in one persistent launch (pa_attn_fwd_split).
+    Calls of one plan over the same tensors must not overlap (they share the sync
+    counters)."""
+
+    kernel = "split"
+
+    def __init__(self, first, second, sched, pool):
+        self.first, self.second, self.sched, self.pool = first, second, sched, pool
+        self.out, self.device = first.out, first.device
+        a = _lib.PaSplitArgs()
+        a.first, a.second = ctypes.pointer(first.args), ctypes.pointer(second.args)
+        a.run_steps, a.run_start, a.run_groups = _lib.ptr(sched.run), _lib.ptr(sched.start), sched.groups
+        a.kv_bits = _lib.ptr(pool)
+        a.sync, a.sync_groups = _lib.ptr(sched.sync), sched.sync_groups
+        a.sync_signal, a.sync_wait = sched.sync_signal, sched.sync_wait
+        a.status = _lib.ptr(sched.status)
+        self.args = a
+        self._ref = ctypes.byref(a)
+
+    def __call__(self):
+        _lib.check(_lib.lib().pa_attn_fwd_split(self._ref, _lib.stream_of(self.out)), "pa_attn_fwd_split")
+        return self.out
 
 
 def lse_merge(o_parts, lse_parts, out_dtype=torch.float32, lse_out=None):

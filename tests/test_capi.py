@@ -80,14 +80,15 @@ def test_product_refuses_host_tensors():
 
 def test_every_struct_field_offset_matches_the_c_compiler(tmp_path):
     """gcc compiles the header and prints offsetof / sizeof of every field of pa_attn_args,
-    pa_mask, pa_term, pa_decode_args and pa_attn_bwd_args; the ctypes mirrors must agree
+    pa_mask, pa_term, pa_decode_args, pa_attn_bwd_args and pa_split_args; the ctypes mirrors must agree
     field by field."""
     import shutil
     import subprocess
     if shutil.which("gcc") is None:
         pytest.skip("gcc not available")
     structs = {"pa_attn_args": _lib.PaAttnArgs, "pa_mask": _lib.PaMask, "pa_term": _lib.PaTerm,
-               "pa_decode_args": _lib.PaDecodeArgs, "pa_attn_bwd_args": _lib.PaAttnBwdArgs}
+               "pa_decode_args": _lib.PaDecodeArgs, "pa_attn_bwd_args": _lib.PaAttnBwdArgs,
+               "pa_split_args": _lib.PaSplitArgs}
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')

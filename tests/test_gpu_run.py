@@ -121,3 +121,56 @@ def test_workloads_persistent_equal_per_block(gpu, name):
     torch.cuda.synchronize()
     assert torch.equal(o_r, o_b), f"{name}: max diff {(o_r.float() - o_b.float()).abs().max().item():.3e}"
     assert torch.equal(lse_r, lse_b)
+
+
+def _split_plans(pieces, N, dev, **kw):
+    fused = SplitPlan(pieces, N, dev, **kw)
+    two = SplitPlan(pieces, N, dev, fuse=False)
+    return fused, two
+
+
+@pytest.mark.parametrize("N,BH,xcds", [(4096, 8, None), (4096, 8, 1), (8192, 3, None), (16384, 16, 1)])
+def test_split_launch_equals_two_launches(gpu, N, BH, xcds):
+    """Both pieces of the band + lattice split in one launch (the lattice merging into the
+    band's rows as they are published) give the two-launch result bit for bit, with the
+    heads spread over the XCDs or not (xcds=1: waits cross XCDs); the counters are left
+    zero and no wait gave up."""
+    band = pm.SlidingWindow(256)
+    lat = pm.Difference(pm.Dilated(16), band)
+    pieces = [Piece(band, 128, 32), Piece(lat, 128, 32, residue=16)]
+    q, k, v = make_qkv(BH, N, 128, torch.bfloat16, seed=N + BH)
+    qd, kd, vd = (x.to(gpu) for x in (q, k, v))
+    fused, two = _split_plans(pieces, N, gpu, split_xcds=xcds)
+    launches, _, _ = fused.prepare(qd, kd, vd)
+    assert [x.kernel for x in launches] == ["split"]
+    lse_f = torch.empty(BH, N, device=gpu)
+    lse_t = torch.empty(BH, N, device=gpu)
+    for _ in range(3):                       # repeated launches reuse the counters
+        o_f = fused.forward(qd, kd, vd, lse=lse_f)
+    o_t = two.forward(qd, kd, vd, lse=lse_t)
+    torch.cuda.synchronize()
+    fused.check()
+    sched = fused._runs[("split", BH)][0]
+    assert int(sched.sync.abs().sum()) == 0 and int(sched.status.item()) == 0
+    assert torch.equal(o_f, o_t), f"max diff {(o_f.float() - o_t.float()).abs().max().item():.3e}"
+    assert torch.equal(lse_f, lse_t)
+    if N <= 8192:
+        want, _ = oatt.dense_attention(as64(q), as64(k), as64(v), oatt.spec_rows(om.NAMED["band256+lat16"], N))
+        check_close(o_f, want, torch.bfloat16, "split launch")
+
+
+def test_split_launch_headline_equals_per_block(gpu):
+    """At the headline size the one-launch split reproduces the per-block kernels bit for bit."""
+    wl = workloads.make("bandlat-L16k")
+    q, k, v = wl.inputs(0, gpu)
+    fused = SplitPlan(wl.pieces, wl.L, gpu)
+    blk = SplitPlan(wl.pieces, wl.L, gpu, persistent=False)
+    launches, _, _ = fused.prepare(q, k, v)
+    assert [x.kernel for x in launches] == ["split"]
+    lse_f = torch.empty(wl.H, wl.L, device=gpu)
+    lse_b = torch.empty(wl.H, wl.L, device=gpu)
+    o_f = fused.forward(q, k, v, lse=lse_f)
+    o_b = blk.forward(q, k, v, lse=lse_b)
+    torch.cuda.synchronize()
+    fused.check()
+    assert torch.equal(o_f, o_b) and torch.equal(lse_f, lse_b)

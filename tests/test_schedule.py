@@ -40,3 +40,70 @@ def test_equal_lengths_go_round_robin_over_neighbouring_blocks():
         first.setdefault(int(g), (int(h), int(q)))
     # XCD 0 owns head 0; its 8 work-groups (0, 8, ..., 56) start on query blocks 0..7
     assert [first[g] for g in range(0, 64, 8)] == [(0, q) for q in range(8)]
+
+
+def test_split_groups_of_band_and_lattice_blocks():
+    """Identity blocks and rp16 blocks of L=16384 meet in 8 groups: 16 consecutive band
+    blocks (2048 rows) and the 16 classes' blocks of the same rows."""
+    from polyhedral_amd.schedule import block_rows, sync_groups
+    N = 16384
+    g0, g1, ng = sync_groups(N // 128, lambda p, qb: block_rows(qb, (0, 16)[p], N))
+    assert ng == 8
+    assert np.array_equal(g0, np.arange(128) // 16)
+    assert np.array_equal(g1, np.arange(128) % 8)
+    for g in range(ng):
+        rows0 = np.concatenate([block_rows(qb, 0, N) for qb in np.flatnonzero(g0 == g)])
+        rows1 = np.concatenate([block_rows(qb, 16, N) for qb in np.flatnonzero(g1 == g)])
+        assert np.array_equal(np.sort(rows0), np.sort(rows1))
+
+
+def _simulate(lists, speed):
+    """Run the work-group lists with every work-group resident: an item of piece 1
+    finishes only after every piece-0 item of its group has; returns the makespan or
+    raises on a cycle (no work-group can progress)."""
+    need = {}
+    for lst in lists:
+        for pc, bh, qb, sg, L in lst:
+            if pc == 0:
+                need[sg] = need.get(sg, 0) + 1
+    done = {sg: 0 for sg in need}
+    pos = [0] * len(lists)
+    t = [0.0] * len(lists)
+    remaining = sum(len(x) for x in lists)
+    while remaining:
+        progressed = False
+        for g, lst in enumerate(lists):
+            while pos[g] < len(lst):
+                pc, bh, qb, sg, L = lst[pos[g]]
+                if pc == 1 and done[sg] < need[sg]:
+                    break
+                t[g] += L / speed[g]
+                if pc == 0:
+                    done[sg] += 1
+                pos[g] += 1
+                remaining -= 1
+                progressed = True
+        if not progressed:
+            raise AssertionError("cycle: no work-group can finish its item")
+    return max(t)
+
+
+@pytest.mark.parametrize("BH,groups,xcds", [(32, 512, 8), (32, 512, 1), (3, 64, 8), (8, 96, 8)])
+def test_split_lists_cover_every_item_in_order_without_cycles(BH, groups, xcds):
+    from polyhedral_amd.schedule import block_rows, split_lists, sync_groups
+    N = 16384
+    g0, g1, ng = sync_groups(N // 128, lambda p, qb: block_rows(qb, (0, 16)[p], N))
+    len0 = np.full(128, 6)
+    len0[:2] = (2, 4)
+    len1 = 2 * (np.arange(128) % 8) + 2
+    lists = split_lists(len0, len1, g0, g1, ng, BH, groups, xcds)
+    items = [it[:4] for lst in lists for it in lst]
+    want = {(0, h, q, h * ng + g0[q]) for h in range(BH) for q in range(128)} | \
+           {(1, h, q, h * ng + g1[q]) for h in range(BH) for q in range(128)}
+    assert len(items) == len(want) and set(items) == want
+    # co-resident work-groups never wait in a cycle, whatever their relative speeds
+    rng = np.random.default_rng(BH)
+    for speed in (np.ones(groups), rng.uniform(0.5, 1.5, groups)):
+        _simulate(lists, speed)
+    ideal = (len0.sum() + len1.sum()) * BH / groups
+    assert _simulate(lists, np.ones(groups)) < 1.25 * ideal + len1.max()
