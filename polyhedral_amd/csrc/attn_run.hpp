@@ -172,7 +172,7 @@ void attn_run_kernel(const AttnK a) {
   // rewriting what it read).  Row pointers include the lane's column offset 4 G, so every
   // column below is an immediate offset: no per-column address stays live across items.
   const bool prev16 = a.prev_o && a.prev_dtype != PA_F32;
-  auto finish = [&](int pc, int bh, int qb, int sg) __attribute__((always_inline)) {
+  auto finish = [&](int pc, int bh, int qb, int sg, int SL) __attribute__((always_inline)) {
     const int flags = a.run_flags[pc];
     const bool merge = (flags & kPieceMerge) != 0;
     const bool signal = a.run_sync && sg >= 0 && !merge;   // publishes rows another piece merges into
@@ -231,12 +231,22 @@ void attn_run_kernel(const AttnK a) {
         lse_v = M + logf(den);
       }
     }
-    char* orow = a.o + ((int64_t)bh * a.o_sb + (int64_t)srow * a.o_sn + 4 * G) * ESZ;
+    // The output rows go through LDS and leave as whole rows, 16 bytes per lane and four
+    // full rows per store instruction (no partial cache lines for the L2 to fill): wave w
+    // stages its 32 rows (8 KB, 16-byte units swizzled as K) in the V slot this step's P.V
+    // read (waves 0, 1) or the K slot its QK read (waves 2, 3), after every wave is past
+    // those reads; the next DMA into them follows the next iteration's barrier.
+    __syncthreads();
+    lds_char_t* stage = (lds_char_t*)smem + (w < 2 ? kVring + SL * kSlot : kKring + (SL ^ 1) * kSlot) + (w & 1) * 8192;
+    typedef __attribute__((address_space(3))) u32x2 lds_w2;
+    // (lane terms made opaque here, so the staging addresses are computed per item
+    // instead of being hoisted out of the step loop into registers)
+    int mx16 = 16 * (m & 15), lx16 = 16 * (lane & 15), rq = lane >> 4;
+    asm volatile("" : "+v"(mx16), "+v"(lx16), "+v"(rq));
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
-        const int d0 = 32 * db + 8 * i4;
         f32x4 x = {acc[db][4 * i4], acc[db][4 * i4 + 1], acc[db][4 * i4 + 2], acc[db][4 * i4 + 3]};
         x *= a_own;
         if (a_prev != 0.f) {
@@ -247,15 +257,28 @@ void attn_run_kernel(const AttnK a) {
                                   : __builtin_convertvector(__builtin_bit_cast(f16x4, pw), f32x4);
             x += a_prev * pvv;
           } else {
-            x += a_prev * load4_any(prow + d0 * 4, PA_F32);
+            x += a_prev * load4_any(prow + (32 * db + 8 * i4) * 4, PA_F32);
           }
         }
-        const u32x2 ov = __builtin_bit_cast(u32x2, Mma<T>::cvt4(x));
-        if (signal)
-          __hip_atomic_store(reinterpret_cast<uint64_t*>(orow + d0 * ESZ), __builtin_bit_cast(uint64_t, ov),
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-          *reinterpret_cast<u32x2*>(orow + d0 * ESZ) = ov;
+        *(lds_w2*)(stage + m * 256 + ((16 * (4 * db + i4)) ^ mx16) + 8 * G) =
+            __builtin_bit_cast(u32x2, Mma<T>::cvt4(x));
+      }
+    }
+    // (each wave reads back only the rows it wrote: LDS keeps a wave's accesses in order)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = 4 * i + rq;
+      const u32x4 v = *(lds_u4*)(stage + rr * 256 + (lx16 ^ (16 * (rr & 15))));
+      const int r_ = qb * 128 + w * 32 + rr;
+      const int s_ = (flags & kPieceScatterO) ? q_orig_of(pc, r_) : r_;
+      char* dst = a.o + ((int64_t)bh * a.o_sb + (int64_t)s_ * a.o_sn) * ESZ + lx16;
+      if (signal) {
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), (uint64_t)v.x | ((uint64_t)v.y << 32), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(dst + 8), (uint64_t)v.z | ((uint64_t)v.w << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        *reinterpret_cast<u32x4*>(dst) = v;
       }
     }
     if (a.lse && G == 0) {
@@ -325,7 +348,7 @@ void attn_run_kernel(const AttnK a) {
       PA_FAST_ORDER();                                                                            \
     }                                                                                             \
     if (fl_c & kRunLast) {                                                                        \
-      finish((fl_c >> 2) & 1, cur_bh, cur_qb, cur_sg);                                            \
+      finish((fl_c >> 2) & 1, cur_bh, cur_qb, cur_sg, (P));                                       \
       cur_bh = d_j1.pad[1];                                                                       \
       cur_qb = fl_n >> kRunQbShift;                                                               \
       cur_sg = d_j1.pad[2];                                                                       \
@@ -419,11 +442,13 @@ void attn_run_kernel(const AttnK a) {
     }
     PA_RITER(j + 1, 1);
   }
-  if (j & 1)
+  if (j & 1) {
     PA_RLAST(1);
-  else
+    finish((fl_c >> 2) & 1, cur_bh, cur_qb, cur_sg, 1);
+  } else {
     PA_RLAST(0);
-  finish((fl_c >> 2) & 1, cur_bh, cur_qb, cur_sg);
+    finish((fl_c >> 2) & 1, cur_bh, cur_qb, cur_sg, 0);
+  }
 
 #undef PA_RITER
 #undef PA_RLAST

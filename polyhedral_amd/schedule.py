@@ -13,10 +13,10 @@ so the step pipeline never drains between items.  This module decides the lists:
 * MI355X dispatches work-group g to XCD g mod 8, and each XCD has its own L2.  When the
   heads split evenly, XCD x gets a contiguous range of heads, so the query blocks that
   share K / V rows share an L2;
-* within an XCD, longest-processing-time first: items in decreasing number of steps,
-  each to the work-group with the least work so far (ties to the lowest index).  Items
-  of equal length then go round robin, so at any moment an XCD's work-groups hold
-  consecutive query blocks of one head.
+* within an XCD, head by head, and within a head longest-processing-time first: items
+  in decreasing number of steps, each to the work-group with the least work so far
+  (ties to the lowest index).  At any moment an XCD's work-groups then hold query
+  blocks of one or two heads, whose K / V the XCD's L2 can serve.
 
 pa_index_run expands the lists into run rows on the device.
 """
@@ -57,15 +57,14 @@ def assign(lengths, BH, groups, keep_empty=True, xcds=XCDS):
         heap = [(0, i, s) for i, s in enumerate(slots)]
         heapq.heapify(heap)
         heads = range(p * per_part_heads, (p + 1) * per_part_heads)
-        # every head's items of one length before the next length: head-major within a
-        # length class, so concurrent work-groups hold neighbouring query blocks
-        for L in np.unique(lens_o)[::-1]:
-            sel = qbs_o[lens_o == L]
-            for bh in heads:
-                for qb in sel:
-                    load, i, s = heapq.heappop(heap)
-                    lists[s].append((bh, int(qb), int(L)))
-                    heapq.heappush(heap, (load + int(L), i, s))
+        # head-major, longest first within a head: the XCD's work-groups work on one head
+        # at a time (its K / V, a few MB, then serves their reads from the XCD's L2), and
+        # the heads' items interleave only at the turn of a head
+        for bh in heads:
+            for qb, L in zip(qbs_o, lens_o):
+                load, i, s = heapq.heappop(heap)
+                lists[s].append((bh, int(qb), int(L)))
+                heapq.heappush(heap, (load + int(L), i, s))
     item_bh, item_qb, item_len, group_of = [], [], [], []
     for g, lst in enumerate(lists):
         for bh, qb, L in lst:

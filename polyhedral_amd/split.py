@@ -54,14 +54,17 @@ class SplitPlan:
     create_block_mask), then reused by every forward.  order="lpt" issues each
     piece's query blocks longest first; None keeps index order."""
 
-    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto", persistent=True, fuse=True,
+    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto", persistent=False, fuse=True,
                  split_xcds=None):
         self.N = N
         self.kernel = kernel
         # persistent: run the streaming pieces on the persistent kernel (a fixed set of
         # work-groups, each a list of items as one stream of steps); fuse: a two-piece
-        # split runs as ONE persistent launch, the second piece merging into the first
-        # piece's rows as soon as they are written (pa_attn_fwd_split)
+        # split then runs as ONE persistent launch, the second piece merging into the first
+        # piece's rows as soon as they are written (pa_attn_fwd_split).  Off by default:
+        # measured on the band + lattice workload, the per-block launches (the hardware
+        # dispatching one work-group per item, in order) keep the L2 hit rate higher than
+        # a static list per work-group, and the passes are bound by their L2-miss bytes
         self.persistent = persistent and kernel != "general"
         self.fuse = fuse and self.persistent
         self.split_xcds = split_xcds   # XCD partition of a split launch's schedule (None: all 8)

@@ -35,14 +35,15 @@ def test_run_rows_follow_the_descriptors(gpu, residue, keep_empty):
     r = 0
     while r < run.rows:
         fl, bh = rows[r, 9], rows[r, 10]
-        qb = fl >> 2
+        qb = fl >> 3
+        assert not fl & 4 and rows[r, 11] == -1       # piece 0, no sync group
         assert fl & 1, f"row {r} does not start an item"
         n = max(1, int(nsteps[qb]))
         assert (bh, qb) not in seen
         seen.add((bh, qb))
         for j in range(n):
             row = rows[r + j]
-            assert row[10] == bh and (row[9] >> 2) == qb
+            assert row[10] == bh and (row[9] >> 3) == qb
             assert (row[9] & 1) == (j == 0) and ((row[9] >> 1) & 1) == (j == n - 1)
             if nsteps[qb] == 0:
                 assert not row[4] and np.all(row[0:4] == bh * N) and np.all(row[5:9] == -1)
@@ -55,7 +56,7 @@ def test_run_rows_follow_the_descriptors(gpu, residue, keep_empty):
 
 
 def _plans(pieces, N, dev):
-    return SplitPlan(pieces, N, dev, persistent=True), SplitPlan(pieces, N, dev, persistent=False)
+    return SplitPlan(pieces, N, dev, persistent=True, fuse=False), SplitPlan(pieces, N, dev, persistent=False)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -94,16 +95,21 @@ def test_persistent_split_with_empty_lists_and_merge(gpu):
     lat = pm.Difference(pm.Dilated(16), band)
     pieces = [Piece(lat, 128, 32, residue=0), Piece(band, 128, 32)]
     q, k, v = make_qkv(BH, N, D, torch.bfloat16, seed=3)
-    run_plan, blk_plan = _plans(pieces, N, gpu)
+    blk_plan = SplitPlan(pieces, N, gpu, persistent=False)
     qd, kd, vd = (x.to(gpu) for x in (q, k, v))
-    launches, _, _ = run_plan.prepare(qd, kd, vd)
-    assert [x.kernel for x in launches] == ["run", "run"]
-    o_r = run_plan.forward(qd, kd, vd)
     o_b = blk_plan.forward(qd, kd, vd)
-    torch.cuda.synchronize()
     want, _ = oatt.dense_attention(as64(q), as64(k), as64(v), oatt.spec_rows(om.NAMED["band256+lat16"], N))
-    check_close(o_r, want, torch.bfloat16, "empty lists + merge")
-    assert torch.equal(o_r, o_b)
+    # two persistent launches, and one split launch (both pieces in the identity basis:
+    # every sync group is one query block of each piece)
+    for plan, kinds in ((SplitPlan(pieces, N, gpu, persistent=True, fuse=False), ["run", "run"]),
+                        (SplitPlan(pieces, N, gpu, persistent=True), ["split"])):
+        launches, _, _ = plan.prepare(qd, kd, vd)
+        assert [x.kernel for x in launches] == kinds
+        o_r = plan.forward(qd, kd, vd)
+        torch.cuda.synchronize()
+        plan.check()
+        check_close(o_r, want, torch.bfloat16, f"empty lists + merge ({kinds})")
+        assert torch.equal(o_r, o_b)
 
 
 @pytest.mark.parametrize("name", ["dilated8-L8k", "bandlat-L16k", "sinkwin-L32k", "prefixlat-L64k"])
@@ -124,8 +130,8 @@ def test_workloads_persistent_equal_per_block(gpu, name):
 
 
 def _split_plans(pieces, N, dev, **kw):
-    fused = SplitPlan(pieces, N, dev, **kw)
-    two = SplitPlan(pieces, N, dev, fuse=False)
+    fused = SplitPlan(pieces, N, dev, persistent=True, **kw)
+    two = SplitPlan(pieces, N, dev, persistent=True, fuse=False)
     return fused, two
 
 
@@ -163,7 +169,7 @@ def test_split_launch_headline_equals_per_block(gpu):
     """At the headline size the one-launch split reproduces the per-block kernels bit for bit."""
     wl = workloads.make("bandlat-L16k")
     q, k, v = wl.inputs(0, gpu)
-    fused = SplitPlan(wl.pieces, wl.L, gpu)
+    fused = SplitPlan(wl.pieces, wl.L, gpu, persistent=True)
     blk = SplitPlan(wl.pieces, wl.L, gpu, persistent=False)
     launches, _, _ = fused.prepare(q, k, v)
     assert [x.kernel for x in launches] == ["split"]
