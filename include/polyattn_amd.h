@@ -278,6 +278,16 @@ typedef struct pa_split_args {
   int32_t sync_signal;
   int32_t sync_wait;
   int32_t* status;
+  /* items != NULL: the split runs as one work-group per item instead of a persistent run
+   * (run_steps / run_start / run_groups / kv_bits then unused, and each piece's args have
+   * run_groups 0 and their kv_steps in index order).  items is int32 [n_items][4] =
+   * (piece, batch-head, query block, sync group), listed in the order the work-groups
+   * are to start (the first-piece items of a group before every second-piece item of
+   * it); the hardware starts work-groups in id order, and work-group i takes item
+   * i' = (i mod 8) * (n / 8) + min(i mod 8, n mod 8) + i div 8 (the items of XCD x are a
+   * contiguous range).  Not cooperative. */
+  const int32_t* items;
+  int64_t n_items;
 } pa_split_args;
 
 int pa_attn_fwd_split(const pa_split_args* args, void* stream);

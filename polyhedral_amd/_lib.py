@@ -14,7 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libpolyattn_amd.s
 PA_OK, PA_E_INVALID, PA_E_HIP, PA_E_UNSUPPORTED = 0, -1, -2, -3
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 MAX_TERMS = 8
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -49,7 +49,7 @@ class PaSplitArgs(ctypes.Structure):
     _fields_ = [("first", ctypes.POINTER(PaAttnArgs)), ("second", ctypes.POINTER(PaAttnArgs)),
                 ("run_steps", c_vp), ("run_start", c_vp), ("run_groups", c_i32), ("kv_bits", c_vp),
                 ("sync", c_vp), ("sync_groups", c_i32), ("sync_signal", c_i32), ("sync_wait", c_i32),
-                ("status", c_vp)]
+                ("status", c_vp), ("items", c_vp), ("n_items", c_i64)]
 
 
 class PaDecodeArgs(ctypes.Structure):

@@ -10,6 +10,7 @@ int launch_attn_f16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f32(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s);
 int launch_attn_run(const AttnK& a, int groups, int dtype, bool cooperative, hipStream_t s);
+int launch_attn_split_grid(const AttnK& a, int dtype, hipStream_t s);
 }  // namespace pa
 
 namespace pa {
@@ -187,10 +188,33 @@ extern "C" int pa_attn_fwd_split(const pa_split_args* x, void* stream) {
   pa::AttnK a, b;
   if (int rc = pa::fill_attn(f, a)) return rc;
   if (int rc = pa::fill_attn(g, b)) return rc;
-  PA_CHECK_ARG(f->run_groups > 0 && g->run_groups == f->run_groups && x->run_groups == f->run_groups &&
-                   f->run_steps == x->run_steps && g->run_steps == x->run_steps && f->run_start == x->run_start &&
-                   g->run_start == x->run_start,
-               "pa_attn_fwd_split: both pieces must be run launches over the split's run rows");
+  const bool grid = x->items != nullptr;
+  if (grid) {
+    // one work-group per item: each piece's own descriptors (index order) and bitmaps
+    PA_CHECK_ARG(x->n_items >= 1 && x->n_items <= 0x7fffffff, "pa_attn_fwd_split: n_items=%lld",
+                 (long long)x->n_items);
+    for (const pa_attn_args* y : {f, g}) {
+      PA_CHECK_ARG(y->run_groups == 0 && y->kv_steps && !y->qblock_order,
+                   "pa_attn_fwd_split: a grid split takes each piece's kv_steps in index order (no run, no order)");
+      PA_CHECK_ARG(y->dtype == PA_BF16 || y->dtype == PA_F16, "pa_attn_fwd_split: f16 or bf16 only");
+      PA_CHECK_ARG(y->D == 128 && y->BQ == 128 && (y->A == 16 || y->A == 32 || y->A == 64),
+                   "pa_attn_fwd_split: D = 128, BQ = 128, A in 16, 32, 64");
+      PA_CHECK_ARG(y->pitch == 0 || y->kv_bits, "pa_attn_fwd_split: the partial-tile bitmaps are needed");
+      PA_CHECK_ARG(!(y->gather_q || y->scatter_o || y->gather_kv) || y->residue_s > 0,
+                   "pa_attn_fwd_split: gathers and scatters go through the closed-form residue basis");
+      PA_CHECK_ARG(y->steps_pitch >= 1 && y->steps_pitch >= (y->pitch * y->A + 63) / 64,
+                   "pa_attn_fwd_split: steps_pitch too small");
+      PA_CHECK_ARG((reinterpret_cast<uintptr_t>(y->kv_steps) & 15) == 0, "pa_attn_fwd_split: kv_steps alignment");
+      const int64_t rb = (y->k_sn > y->v_sn ? y->k_sn : y->v_sn) * 2;
+      PA_CHECK_ARG(y->N * rb < (1ll << 31) && y->N * y->o_sn * 2 < (1ll << 31),
+                   "pa_attn_fwd_split: N * row stride too large");
+    }
+  } else {
+    PA_CHECK_ARG(f->run_groups > 0 && g->run_groups == f->run_groups && x->run_groups == f->run_groups &&
+                     f->run_steps == x->run_steps && g->run_steps == x->run_steps && f->run_start == x->run_start &&
+                     g->run_start == x->run_start,
+                 "pa_attn_fwd_split: both pieces must be run launches over the split's run rows");
+  }
   PA_CHECK_ARG(f->q == g->q && f->k == g->k && f->v == g->v && f->o == g->o && f->lse == g->lse &&
                    f->q_sb == g->q_sb && f->q_sn == g->q_sn && f->k_sb == g->k_sb && f->k_sn == g->k_sn &&
                    f->v_sb == g->v_sb && f->v_sn == g->v_sn && f->o_sb == g->o_sb && f->o_sn == g->o_sn &&
@@ -201,11 +225,11 @@ extern "C" int pa_attn_fwd_split(const pa_split_args* x, void* stream) {
   PA_CHECK_ARG(g->prev_o == f->o && g->prev_lse == f->lse && g->prev_dtype == f->dtype && g->prev_sb == f->o_sb &&
                    g->prev_sn == f->o_sn,
                "pa_attn_fwd_split: the second piece merges into the first piece's o and lse");
-  PA_CHECK_ARG(x->kv_bits || (f->pitch == 0 && g->pitch == 0), "pa_attn_fwd_split: null kv_bits");
+  PA_CHECK_ARG(grid || x->kv_bits || (f->pitch == 0 && g->pitch == 0), "pa_attn_fwd_split: null kv_bits");
   PA_CHECK_ARG(x->sync && x->status && x->sync_groups >= 1 && x->sync_signal >= 1 && x->sync_wait >= 1,
                "pa_attn_fwd_split: sync=%p status=%p groups=%d signal=%d wait=%d", (void*)x->sync,
                (void*)x->status, x->sync_groups, x->sync_signal, x->sync_wait);
-  a.kv_bits = x->kv_bits;
+  if (!grid) a.kv_bits = x->kv_bits;
   a.run_res[1] = b.run_res[0];
   a.run_qlog2[1] = b.run_qlog2[0];
   a.run_flags[1] = b.run_flags[0];
@@ -219,5 +243,13 @@ extern "C" int pa_attn_fwd_split(const pa_split_args* x, void* stream) {
   a.run_sync_signal = x->sync_signal;
   a.run_sync_wait = x->sync_wait;
   a.run_status = x->status;
+  if (grid) {
+    a.split_items = x->items;
+    a.total_wg = x->n_items;
+    a.steps1 = g->kv_steps;
+    a.steps_pitch1 = g->steps_pitch;
+    a.kv_bits1 = g->kv_bits;
+    return pa::launch_attn_split_grid(a, f->dtype, static_cast<hipStream_t>(stream));
+  }
   return pa::launch_attn_run(a, x->run_groups, f->dtype, true, static_cast<hipStream_t>(stream));
 }

@@ -90,6 +90,11 @@ struct AttnK {
   int32_t* run_sync;                 // [2 * run_sync_groups]: items finished, merges done
   int32_t run_sync_groups, run_sync_signal, run_sync_wait;
   int32_t* run_status;               // set to 1 when a merge gives up waiting
+  // attn_stream_kernel<T, true>: a two-piece split in one grid, one work-group per item
+  const int32_t* split_items;        // [total_wg][4]: piece, batch-head, query block, sync group
+  const int32_t* steps1;             // piece 1's step descriptors (index order), its pitch and
+  int64_t steps_pitch1;              //   bitmap pool (piece 0's are steps / steps_pitch / kv_bits)
+  const uint32_t* kv_bits1;
 };
 
 // flags of a piece of a persistent run (AttnK::run_flags)
@@ -212,6 +217,18 @@ __device__ __forceinline__ void dma_x1(uint32_t m0, const char* gbase, uint32_t 
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
 }
 __device__ __forceinline__ void dma_wait_all() { asm volatile("s_waitcnt vmcnt(0)"); }
+// The same DMA with agent-scope coherence (sc1): reads data another work-group published
+// with agent-scope stores, whichever XCD's L2 it went through.
+__device__ __forceinline__ void dma_x4_sc1(uint32_t m0, const char* gbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 sc1" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+}
+// A 16-byte agent-scope store (sc1: written through to memory, visible to every XCD once
+// complete); the caller waits for it (s_waitcnt vmcnt) before publishing.
+__device__ __forceinline__ void store_x4_sc1(char* p, uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
+  typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+  const v4 v = {x, y, z, w};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
 
 // Uniform description of the 4 segments (16 index-space KV rows each) of one step.
 struct StepMeta {

@@ -20,12 +20,12 @@ static int raise_lds_limit(K kernel, unsigned long long& configured, const char*
   return PA_OK;
 }
 
-template <typename T>
+template <typename T, bool SPLIT>
 static int launch_stream_t(const AttnK& a, hipStream_t s, const char* name) {
   static unsigned long long configured = 0ull;
-  if (int rc = raise_lds_limit(&attn_stream_kernel<T>, configured, "hipFuncSetAttribute(attn_stream_kernel)"))
+  if (int rc = raise_lds_limit(&attn_stream_kernel<T, SPLIT>, configured, "hipFuncSetAttribute(attn_stream_kernel)"))
     return rc;
-  hipLaunchKernelGGL(attn_stream_kernel<T>, dim3((unsigned)a.total_wg), dim3(256), kStreamSmem, s, a);
+  hipLaunchKernelGGL((attn_stream_kernel<T, SPLIT>), dim3((unsigned)a.total_wg), dim3(256), kStreamSmem, s, a);
   PA_LAUNCH_CHECK(name);
   return PA_OK;
 }
@@ -59,8 +59,13 @@ static int launch_run_t(const AttnK& a, int groups, bool cooperative, hipStream_
 }
 
 int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s) {
-  if (dtype == PA_BF16) return launch_stream_t<__bf16>(a, s, "attn_stream_kernel<bf16>");
-  return launch_stream_t<_Float16>(a, s, "attn_stream_kernel<f16>");
+  if (dtype == PA_BF16) return launch_stream_t<__bf16, false>(a, s, "attn_stream_kernel<bf16>");
+  return launch_stream_t<_Float16, false>(a, s, "attn_stream_kernel<f16>");
+}
+
+int launch_attn_split_grid(const AttnK& a, int dtype, hipStream_t s) {
+  if (dtype == PA_BF16) return launch_stream_t<__bf16, true>(a, s, "attn_stream_kernel<bf16, split>");
+  return launch_stream_t<_Float16, true>(a, s, "attn_stream_kernel<f16, split>");
 }
 
 int launch_attn_run(const AttnK& a, int groups, int dtype, bool cooperative, hipStream_t s) {

@@ -50,6 +50,8 @@ constexpr int kVring = 4096;
 constexpr int kKring = 36864;
 constexpr int kSlot = 16384;
 constexpr int kStreamSmem = kKring + 2 * kSlot;
+// polls of a split grid's sync count before a merge gives up (each ~0.5 us)
+constexpr int kSplitMaxPolls = 1 << 20;
 
 template <typename T>
 __device__ __forceinline__ float dot2_sum(uint32_t packed, float acc);
@@ -66,7 +68,14 @@ __device__ __forceinline__ float dot2_sum<_Float16>(uint32_t packed, float acc) 
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), one, acc, false);
 }
 
-template <typename T>
+// SPLIT: the grid holds the items of both pieces of a disjoint split (AttnK::split_items,
+// in the order the work-groups are dispatched).  A first-piece item publishes its output
+// rows and log-sum-exp with agent-scope stores and counts itself in its sync group; a
+// second-piece item waits for its group's count before it reads those rows to merge them.
+// Work-groups are dispatched in id order and the items a second-piece item waits for have
+// lower ids, so they are running or done when it waits; the wait is also bounded (a merge
+// that gives up sets *run_status).  The last merge of a group zeroes the group's counters.
+template <typename T, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_stream_kernel(const AttnK a) {
   constexpr int D = 128;
@@ -86,33 +95,57 @@ void attn_stream_kernel(const AttnK a) {
 
   // (32-bit index arithmetic: the grid is below 2^31 work-groups, checked on the host)
   const uint32_t lid = xcd_remap32(blockIdx.x, (uint32_t)a.total_wg);
-  const uint32_t bh_l = lid / (uint32_t)a.nq;
-  const int64_t bh = a.heads_desc ? a.BH - 1 - bh_l : bh_l;
-  const int qb_lin = (int)(lid - bh_l * (uint32_t)a.nq);
-  // The lists are laid out in issue order; a list's first descriptor names its query
-  // block and its length, so one scalar load starts the work-group.
-  const StepDesc* desc = reinterpret_cast<const StepDesc*>(a.steps) + (int64_t)qb_lin * a.steps_pitch;
   typedef const __attribute__((address_space(4))) int32_t cint;
+  int64_t bh;
+  int pc = 0, sg = -1;
+  const StepDesc* desc;
+  if constexpr (SPLIT) {
+    // the item of this work-group and its piece's descriptors (index order)
+    cint* it = (cint*)a.split_items + 4 * (int64_t)lid;
+    pc = it[0];
+    bh = it[1];
+    sg = it[3];
+    desc = reinterpret_cast<const StepDesc*>(pc ? a.steps1 : a.steps) + (int64_t)it[2] * (pc ? a.steps_pitch1 : a.steps_pitch);
+  } else {
+    const uint32_t bh_l = lid / (uint32_t)a.nq;
+    bh = a.heads_desc ? a.BH - 1 - bh_l : bh_l;
+    const int qb_lin = (int)(lid - bh_l * (uint32_t)a.nq);
+    // The lists are laid out in issue order; a list's first descriptor names its query
+    // block and its length, so one scalar load starts the work-group.
+    desc = reinterpret_cast<const StepDesc*>(a.steps) + (int64_t)qb_lin * a.steps_pitch;
+  }
   const int qb = ((cint*)desc)[13];
   const int n_steps = ((cint*)desc)[14];
   const int A = a.A;
 
-  const bool closed = a.residue_s != 0;
-  const int32_t rmask = (1 << a.residue_qlog2) - 1;
-  const bool has_pq = closed || a.pred.perm_q;
-  const bool gather_kv = a.gather_kv && closed;
-  const int rstride = gather_kv ? a.residue_s : 1;
+  // the piece's basis and role: the launch's arguments, or in a split grid those of the
+  // item's piece (the second piece merges into the first piece's output and log-sum-exp)
+  const int res_s = SPLIT ? a.run_res[pc] : a.residue_s;
+  const int res_q = SPLIT ? a.run_qlog2[pc] : a.residue_qlog2;
+  const int pflags = SPLIT ? a.run_flags[pc] : 0;
+  const bool g_q = SPLIT ? (pflags & kPieceGatherQ) != 0 : a.gather_q != 0;
+  const bool g_kv = SPLIT ? (pflags & kPieceGatherKV) != 0 : a.gather_kv != 0;
+  const bool sc_o = SPLIT ? (pflags & kPieceScatterO) != 0 : a.scatter_o != 0;
+  const char* prev_o = (!SPLIT || (pflags & kPieceMerge)) ? a.prev_o : nullptr;
+  const bool signal = SPLIT && pc == 0;
+  const bool waits = SPLIT && pc == 1;
+
+  const bool closed = res_s != 0;
+  const int32_t rmask = (1 << res_q) - 1;
+  const bool has_pq = closed || (!SPLIT && a.pred.perm_q);
+  const bool gather_kv = g_kv && closed;
+  const int rstride = gather_kv ? res_s : 1;
 
   const int r_idx = qb * 128 + w * 32 + m;  // index-space query row of this lane
   int q_orig = r_idx;
-  if (has_pq) q_orig = closed ? (r_idx & rmask) * a.residue_s + (r_idx >> a.residue_qlog2) : a.pred.perm_q[r_idx];
-  const int r_load = (a.gather_q && has_pq) ? q_orig : r_idx;
+  if (has_pq) q_orig = closed ? (r_idx & rmask) * res_s + (r_idx >> res_q) : a.pred.perm_q[r_idx];
+  const int r_load = (g_q && has_pq) ? q_orig : r_idx;
 
   const char* kbase = a.k + bh * a.k_sb * ESZ;
   const char* vbase = a.v + bh * a.v_sb * ESZ;
   // row offsets inside a head fit in 32 bits (checked on the host)
   const uint32_t krow_b32 = (uint32_t)(a.k_sn * ESZ), vrow_b32 = (uint32_t)(a.v_sn * ESZ);
-  const char* bits = reinterpret_cast<const char*>(a.kv_bits);
+  const char* bits = reinterpret_cast<const char*>(SPLIT && pc ? a.kv_bits1 : a.kv_bits);
   const int wpr = (A + 31) >> 5;
 
   // ---- DMA geometry (loop invariant) ----------------------------------------
@@ -129,12 +162,12 @@ void attn_stream_kernel(const AttnK a) {
   // The previous partial (2-byte types, rows in index order or through the closed-form
   // basis) is DMAed into the K ring at the end of the list: rows 0..63 of the block while
   // the last iteration runs, rows 64..127 at the last step; 16-row segments as for K.
-  const bool prev16 = a.prev_o && a.prev_dtype != PA_F32;
-  const bool prev_dma = prev16 && !(a.scatter_o && has_pq && !closed);
-  const bool prev_closed = a.scatter_o && closed;
+  const bool prev16 = prev_o && a.prev_dtype != PA_F32;
+  const bool prev_dma = prev16 && !(sc_o && has_pq && !closed);
+  const bool prev_closed = sc_o && closed;
   const uint32_t p_goff =
-      (uint32_t)(rs * (prev_closed ? a.residue_s : 1)) * (uint32_t)(a.prev_sn * 2) + 16u * (uint32_t)(pu ^ rs);
-  const char* pbase = a.prev_o + bh * a.prev_sb * 2;
+      (uint32_t)(rs * (prev_closed ? res_s : 1)) * (uint32_t)(a.prev_sn * 2) + 16u * (uint32_t)(pu ^ rs);
+  const char* pbase = prev_o + bh * a.prev_sb * 2;
 
   // ---- LDS read geometry (loop invariant; slot / block / chunk offsets are immediates)
   // QK: lane (m, G) reads K row 32 lb + m, unit 2 kc + G.
@@ -211,8 +244,11 @@ void attn_stream_kernel(const AttnK a) {
   do {                                                                                            \
     _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                               \
       const int r_ = qb * 128 + 64 * (h) + 16 * t;                                                \
-      const int pr_ = prev_closed ? (r_ & rmask) * a.residue_s + (r_ >> a.residue_qlog2) : r_;    \
-      dma_x4(lds0 + kKring + (SL) * kSlot + (16 * t + 4 * w) * 256, pbase + (int64_t)pr_ * a.prev_sn * 2, p_goff); \
+      const int pr_ = prev_closed ? (r_ & rmask) * res_s + (r_ >> res_q) : r_;                    \
+      if (waits)                                                                                  \
+        dma_x4_sc1(lds0 + kKring + (SL) * kSlot + (16 * t + 4 * w) * 256, pbase + (int64_t)pr_ * a.prev_sn * 2, p_goff); \
+      else                                                                                        \
+        dma_x4(lds0 + kKring + (SL) * kSlot + (16 * t + 4 * w) * 256, pbase + (int64_t)pr_ * a.prev_sn * 2, p_goff); \
     }                                                                                             \
   } while (0)
 
@@ -226,10 +262,12 @@ void attn_stream_kernel(const AttnK a) {
   do {                                                                                            \
     dma_wait_all();                                                                               \
     __syncthreads();                                                                              \
-    if ((jj) + 2 < n_steps)                                                                       \
+    if ((jj) + 2 < n_steps) {                                                                     \
       PA_DMA_K(d_j2, (P));                                                                        \
-    else if (prev_dma)                                                                            \
+    } else if (prev_dma) {                                                                        \
+      PA_SPLIT_WAIT();                                                                            \
       PA_DMA_PREV(0, (P));                                                                        \
+    }                                                                                             \
     PA_DMA_V(d_j1, (P) ^ 1);                                                                      \
     StepDesc d_j3{};                                                                              \
     if ((jj) + 3 < n_steps) d_j3 = load_desc((jj) + 3);                                           \
@@ -272,9 +310,10 @@ void attn_stream_kernel(const AttnK a) {
     dma_wait_all();                                                                               \
     __syncthreads();                                                                              \
     if (prev_dma) {                                                                               \
+      PA_SPLIT_WAIT();                                                                            \
       if (n_steps == 1) PA_DMA_PREV(0, (P) ^ 1);                                                  \
       PA_DMA_PREV(1, (P));                                                                        \
-      if (a.prev_o) prev_lse = a.prev_lse[bh * a.lse_sb + srow];                                  \
+      PA_PREV_LSE();                                                                              \
     } else {                                                                                      \
       PA_PREV_LOAD();                                                                             \
     }                                                                                             \
@@ -294,16 +333,51 @@ void attn_stream_kernel(const AttnK a) {
 
   // Rows of the previous partial (prev_o, 2-byte types): 4 elements per (db, i4), the
   // columns this lane writes in the epilogue.
-  const int srow = (a.scatter_o && has_pq) ? q_orig : r_idx;
+  const int srow = (sc_o && has_pq) ? q_orig : r_idx;
   uint2 prevw[NDB * 4];
   float prev_lse = -INFINITY;
+  // A second-piece item of a split grid waits, before its first read of the merge
+  // input, until every first-piece item of its sync group has published its rows
+  // (thread 0 polls the group's count; the barrier releases the work-group).
+  bool waited = false;
+#define PA_SPLIT_WAIT()                                                                           \
+  do {                                                                                            \
+    if (waits && !waited) {                                                                       \
+      if (tid == 0) {                                                                             \
+        int polls_ = 0;                                                                           \
+        while (__hip_atomic_load(a.run_sync + sg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <   \
+               a.run_sync_signal) {                                                               \
+          if (++polls_ >= kSplitMaxPolls ||                                                       \
+              __hip_atomic_load(a.run_status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) { \
+            __hip_atomic_store(a.run_status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);      \
+            break;                                                                                \
+          }                                                                                       \
+          __builtin_amdgcn_s_sleep(16);                                                           \
+        }                                                                                         \
+      }                                                                                           \
+      __syncthreads();                                                                            \
+      waited = true;                                                                              \
+    }                                                                                             \
+  } while (0)
+#define PA_PREV_LSE()                                                                             \
+  do {                                                                                            \
+    if (prev_o) {                                                                                 \
+      const float* lp_ = a.prev_lse + bh * a.lse_sb + srow;                                       \
+      prev_lse = waits ? __hip_atomic_load(lp_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *lp_; \
+    }                                                                                             \
+  } while (0)
 #define PA_PREV_LOAD()                                                                            \
   do {                                                                                            \
-    if (a.prev_o) prev_lse = a.prev_lse[bh * a.lse_sb + srow];                                    \
+    PA_SPLIT_WAIT();                                                                              \
+    PA_PREV_LSE();                                                                                \
     if (prev16) {                                                                                 \
-      const char* prow_ = a.prev_o + (bh * a.prev_sb + (int64_t)srow * a.prev_sn) * 2;             \
-      _Pragma("unroll") for (int q_ = 0; q_ < NDB * 4; ++q_)                                      \
-        prevw[q_] = *reinterpret_cast<const uint2*>(prow_ + (32 * (q_ >> 2) + 8 * (q_ & 3) + 4 * G) * 2); \
+      const char* prow_ = prev_o + (bh * a.prev_sb + (int64_t)srow * a.prev_sn) * 2;               \
+      _Pragma("unroll") for (int q_ = 0; q_ < NDB * 4; ++q_) {                                    \
+        const uint2* at_ = reinterpret_cast<const uint2*>(prow_ + (32 * (q_ >> 2) + 8 * (q_ & 3) + 4 * G) * 2); \
+        prevw[q_] = waits ? __builtin_bit_cast(uint2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(at_), \
+                                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) \
+                          : *at_;                                                                 \
+      }                                                                                           \
     }                                                                                             \
   } while (0)
 
@@ -368,6 +442,8 @@ void attn_stream_kernel(const AttnK a) {
 #undef PA_ITER
 #undef PA_LAST
 #undef PA_PREV_LOAD
+#undef PA_PREV_LSE
+#undef PA_SPLIT_WAIT
 #undef PA_FAST_ORDER
 #undef PA_PV
 #undef PA_EXP
@@ -388,7 +464,7 @@ void attn_stream_kernel(const AttnK a) {
   float lse_v = has ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
   float a_own = has ? 1.f / l_tot : 0.f;
   float a_prev = 0.f;
-  if (a.prev_o) {
+  if (prev_o) {
     const float lp = prev_lse;
     const float M = fmaxf(lse_v, lp);
     if (M == -INFINITY) {
@@ -410,7 +486,7 @@ void attn_stream_kernel(const AttnK a) {
   lds_char_t* stage = (lds_char_t*)smem + kVring + w * 8192;
   typedef __attribute__((address_space(3))) u32x2 lds_w2;
   const int psz = a.prev_dtype == PA_F32 ? 4 : 2;
-  const char* prow = a.prev_o ? a.prev_o + (bh * a.prev_sb + (int64_t)srow * a.prev_sn) * psz : nullptr;
+  const char* prow = prev_o ? prev_o + (bh * a.prev_sb + (int64_t)srow * a.prev_sn) * psz : nullptr;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -433,17 +509,41 @@ void attn_stream_kernel(const AttnK a) {
           __builtin_bit_cast(u32x2, Mma<T>::cvt4(x));
     }
   }
-  if (a.lse && G == 0) a.lse[bh * a.lse_sb + srow] = lse_v;
+  if (a.lse && G == 0) {
+    float* lo_ = a.lse + bh * a.lse_sb + srow;
+    if (signal)
+      __hip_atomic_store(lo_, lse_v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      *lo_ = lse_v;
+  }
   // (each wave reads back only the rows it wrote: LDS keeps a wave's accesses in order)
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int rr = 4 * i + (lane >> 4);
     const u32x4 v = *(lds_u4*)(stage + rr * 256 + 16 * ((lane & 15) ^ (rr & 15)));
     const int r_ = qb * 128 + w * 32 + rr;
-    const int s_ = (a.scatter_o && has_pq)
-                       ? (closed ? (r_ & rmask) * a.residue_s + (r_ >> a.residue_qlog2) : a.pred.perm_q[r_])
-                       : r_;
-    *reinterpret_cast<u32x4*>(a.o + (bh * a.o_sb + (int64_t)s_ * a.o_sn) * ESZ + 16 * (lane & 15)) = v;
+    const int s_ = (sc_o && has_pq) ? (closed ? (r_ & rmask) * res_s + (r_ >> res_q) : a.pred.perm_q[r_]) : r_;
+    char* dst_ = a.o + (bh * a.o_sb + (int64_t)s_ * a.o_sn) * ESZ + 16 * (lane & 15);
+    if (signal)
+      store_x4_sc1(dst_, v.x, v.y, v.z, v.w);
+    else
+      *reinterpret_cast<u32x4*>(dst_) = v;
+  }
+  if constexpr (SPLIT) {
+    if (signal) {
+      // the rows are complete in memory before the group counts them
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0) __hip_atomic_fetch_add(a.run_sync + sg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (tid == 0) {
+      // the last merge of the group zeroes both counters for the next launch
+      const int done = __hip_atomic_fetch_add(a.run_sync + a.run_sync_groups + sg, 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      if (done == a.run_sync_wait - 1) {
+        __hip_atomic_store(a.run_sync + sg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.run_sync + a.run_sync_groups + sg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
 }
 

@@ -259,3 +259,99 @@ class SplitSchedule:
             self.status.zero_()
             self.sync.zero_()
             raise RuntimeError("a merge of the split launch gave up waiting for its rows: results are invalid")
+
+
+def split_grid_items(len0, len1, g0, g1, ng, BH, xcds=None, lag=1):
+    """Items of a two-piece split run as one work-group per item (pa_attn_fwd_split with
+    items): int32 [n, 4] = (piece, batch-head, query block, sync group), in the order the
+    work-groups start.  Work-group ids are dealt to the XCDs in contiguous ranges, so when
+    the heads split evenly the items of XCD x are its heads' items.  Per head, the groups
+    go in decreasing order of second-piece work; each group's first-piece items come
+    `lag` groups before its second-piece items, so a merge rarely finds its rows
+    unpublished.  Within a group, longest list first.  The rows are the items in slot
+    order (the kernel's work-group i takes slot grid_start_order's inverse of i)."""
+    xcds = XCDS if xcds is None else xcds
+    blocks0 = [np.flatnonzero(g0 == g) for g in range(ng)]
+    blocks1 = [np.flatnonzero(g1 == g) for g in range(ng)]
+    gorder = sorted(range(ng), key=lambda g: (-int(len1[blocks1[g]].sum()), g))
+    out = []
+    for bh in range(BH):
+        pend = []
+        for g in gorder:
+            b0 = sorted(blocks0[g], key=lambda q: (-int(len0[q]), int(q)))
+            out += [(0, bh, int(q), bh * ng + g) for q in b0]
+            pend.append(g)
+            if len(pend) > lag:
+                h = pend.pop(0)
+                b1 = sorted(blocks1[h], key=lambda q: (-int(len1[q]), int(q)))
+                out += [(1, bh, int(q), bh * ng + h) for q in b1]
+        for h in pend:
+            b1 = sorted(blocks1[h], key=lambda q: (-int(len1[q]), int(q)))
+            out += [(1, bh, int(q), bh * ng + h) for q in b1]
+    seq = np.asarray(out, dtype=np.int32).reshape(-1, 4)
+    if BH % xcds == 0:
+        # every head has the same number of items, so XCD x's contiguous range of item
+        # slots holds whole heads, each in its own sequence order
+        return seq
+    # otherwise a head would straddle two XCDs' ranges and a merge could start before the
+    # items it waits for: give the sequence to the work-groups in start order instead
+    items = np.empty_like(seq)
+    items[np.argsort(grid_start_order(seq.shape[0]))] = seq
+    return items
+
+
+def grid_start_order(n):
+    """Work-group id (start order) of each of n items: work-group i takes item
+    (i mod 8) * (n // 8) + min(i mod 8, n mod 8) + i // 8 (contiguous item ranges per XCD)."""
+    per, rem = divmod(n, XCDS)
+    hw = np.arange(n, dtype=np.int64)
+    x, r = hw % XCDS, hw // XCDS
+    lid = x * per + np.minimum(x, rem) + r
+    out = np.empty(n, dtype=np.int64)
+    out[lid] = hw
+    return out
+
+
+class SplitGrid:
+    """The items, counters and give-up flag of a two-piece split run as one work-group
+    per item (pa_attn_fwd_split with items).  The two pieces' descriptors must be in
+    index order."""
+
+    def __init__(self, steps0, steps1, residue0, residue1, N, BH, lag=1):
+        dev = steps0.device
+        nq = steps0.shape[0]
+        if steps1.shape[0] != nq:
+            raise ValueError("the pieces must share the query tile")
+        g0, g1, ng = sync_groups(nq, lambda p, qb: block_rows(qb, (residue0, residue1)[p], N))
+        sig = np.bincount(g0, minlength=ng)
+        wai = np.bincount(g1, minlength=ng)
+        if sig.min() != sig.max() or wai.min() != wai.max():
+            raise ValueError("the pieces' query blocks do not form groups of one size")
+        self.sync_signal, self.sync_wait, self.groups_per_head = int(sig[0]), int(wai[0]), ng
+        len0 = np.maximum(steps0[:, 0, 14].cpu().numpy().astype(np.int64), 1)
+        len1 = np.maximum(steps1[:, 0, 14].cpu().numpy().astype(np.int64), 1)
+        items = split_grid_items(len0, len1, g0, g1, ng, BH, lag=lag)
+        # Deadlock freedom: work-groups start in id order, so every second-piece item must
+        # start after all the first-piece items of its group (a wait on a later work-group
+        # could hold a slot that work-group needs).
+        hw = grid_start_order(items.shape[0])
+        first_start = np.full(BH * ng, -1, dtype=np.int64)
+        np.maximum.at(first_start, items[items[:, 0] == 0, 3], hw[items[:, 0] == 0])
+        sec = items[:, 0] == 1
+        if np.any(hw[sec] <= first_start[items[sec, 3]]):
+            raise ValueError("the split grid would start a merge before the items it waits for")
+        self.items = torch.from_numpy(items).to(dev)
+        self.n_items = items.shape[0]
+        self.BH, self.N = BH, N
+        self.residues = (residue0, residue1)
+        self.sync_groups = BH * ng
+        self.sync = torch.zeros(2 * self.sync_groups, dtype=torch.int32, device=dev)
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def check(self):
+        """Raise if a merge of a past launch gave up waiting (its results are invalid);
+        the counters and the flag are cleared for the next launch."""
+        if int(self.status.item()):
+            self.status.zero_()
+            self.sync.zero_()
+            raise RuntimeError("a merge of the split launch gave up waiting for its rows: results are invalid")

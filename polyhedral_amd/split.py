@@ -30,7 +30,7 @@ from .attention import prepare
 from .index import STREAM_TILES, build_device, build_steps
 from .perm import residue_perm
 from .polyattn.masks import Permuted
-from .schedule import RunSchedule, SplitSchedule
+from .schedule import RunSchedule, SplitGrid, SplitSchedule
 from .spec import MaskSpec
 
 
@@ -54,20 +54,23 @@ class SplitPlan:
     create_block_mask), then reused by every forward.  order="lpt" issues each
     piece's query blocks longest first; None keeps index order."""
 
-    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto", persistent=False, fuse=True,
-                 split_xcds=None):
+    def __init__(self, pieces, N, device=None, order="lpt", kernel="auto", persistent=False, fuse=False,
+                 split_xcds=None, split_lag=1):
         self.N = N
         self.kernel = kernel
         # persistent: run the streaming pieces on the persistent kernel (a fixed set of
-        # work-groups, each a list of items as one stream of steps); fuse: a two-piece
-        # split then runs as ONE persistent launch, the second piece merging into the first
-        # piece's rows as soon as they are written (pa_attn_fwd_split).  Off by default:
+        # work-groups, each a list of items as one stream of steps).  Off by default:
         # measured on the band + lattice workload, the per-block launches (the hardware
         # dispatching one work-group per item, in order) keep the L2 hit rate higher than
-        # a static list per work-group, and the passes are bound by their L2-miss bytes
+        # a static list per work-group, and the passes are bound by their L2-miss bytes.
+        # fuse: a two-piece split runs as ONE launch (pa_attn_fwd_split), the second piece
+        # merging into the first piece's rows as soon as they are written: a persistent
+        # run when persistent is set, else one work-group per item in a sequence that puts
+        # each group's first-piece items before its merges
         self.persistent = persistent and kernel != "general"
-        self.fuse = fuse and self.persistent
+        self.fuse = fuse and kernel != "general"
         self.split_xcds = split_xcds   # XCD partition of a split launch's schedule (None: all 8)
+        self.split_lag = split_lag     # groups between a group's first- and second-piece items
         self._runs = {}
         self.pieces = list(pieces)
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
@@ -92,7 +95,7 @@ class SplitPlan:
             steps = (build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], N, p.BQ, p.A,
                                  _closed_form_residue(p, N), qorder) if stream else None)
             # the persistent kernel's run rows come from the descriptors in index order
-            runnable = stream and self.persistent and (perm_t is None or _closed_form_residue(p, N) > 0)
+            runnable = stream and (self.persistent or self.fuse) and (perm_t is None or _closed_form_residue(p, N) > 0)
             steps_idx = (build_steps(kv_idx, kv_num, kv_partial, wave, bits[0], N, p.BQ, p.A,
                                      _closed_form_residue(p, N), None) if runnable else None)
             self.built.append(dict(piece=p, spec=MaskSpec(tuple(inc), tuple(exc)), perm=perm_t,
@@ -145,10 +148,13 @@ class SplitPlan:
         return launches, o, lse_buf
 
     def _fused_launch(self, q, k, v, scale, o, lse_buf):
-        """The whole forward of a two-piece split as one persistent launch, or None when
-        this plan or these tensors do not allow it (then one launch per piece)."""
+        """The whole forward of a two-piece split as one launch (persistent, or one
+        work-group per item), or None when this plan or these tensors do not allow it
+        (then one launch per piece)."""
         if not (self.fuse and len(self.built) == 2):
             return None
+        if not self.persistent:
+            return self._grid_launch(q, k, v, scale, o, lse_buf)
         b0, b1 = self.built
         if b0["live"] == 0 or b1["live"] == 0 or (b0["piece"].BQ, b1["piece"].BQ) != (128, 128):
             return None
@@ -182,11 +188,44 @@ class SplitPlan:
                 kv_steps=b["steps"], kernel=self.kernel, run=(sched, i)))
         return SplitLaunch(ls[0], ls[1], sched, pool)
 
+    def _grid_launch(self, q, k, v, scale, o, lse_buf):
+        b0, b1 = self.built
+        if b0["live"] == 0 or b1["live"] == 0 or (b0["piece"].BQ, b1["piece"].BQ) != (128, 128):
+            return None
+        if b0["piece"].A != b1["piece"].A or b0["steps_idx"] is None or b1["steps_idx"] is None:
+            return None
+        BH, N, D = q.shape
+        if q.dtype not in (torch.float16, torch.bfloat16) or D != 128:
+            return None
+        key = ("grid", BH)
+        if key not in self._runs:
+            try:
+                self._runs[key] = SplitGrid(b0["steps_idx"], b1["steps_idx"], _closed_form_residue(b0["piece"], N),
+                                            _closed_form_residue(b1["piece"], N), N, BH, lag=self.split_lag)
+            except ValueError:
+                self._runs[key] = None
+        grid = self._runs[key]
+        if grid is None:
+            return None
+        ls = []
+        for i, b in enumerate((b0, b1)):
+            p = b["piece"]
+            permuted = b["perm"] is not None
+            ls.append(prepare(
+                q, k, v, b["kv_idx"], b["kv_num"], b["kv_partial"], b["spec"], 0, 0, 0, p.BQ, p.A,
+                scale=scale, perm_q=b["perm"], perm_kv=b["perm"], gather_kv=permuted,
+                kv_wave_bits=b["wave"], kv_bits=b["bits"], gather_q=permuted, scatter_o=permuted,
+                residue=_closed_form_residue(p, N), lse=lse_buf, prev=None if i == 0 else (o, lse_buf), out=o,
+                kv_steps=b["steps_idx"], kernel="stream"))
+        return SplitLaunch(ls[0], ls[1], grid, None)
+
     def check(self):
         """Raise if a merge of a past split launch gave up waiting (see SplitSchedule.check)."""
         for key, val in self._runs.items():
             if key[0] == "split" and val[0] is not None:
                 val[0].check()
+            if key[0] == "grid" and val is not None:
+                val.check()
 
     def _runnable(self, q, k, v, b):
         """Whether the persistent kernel takes this piece over these tensors."""
@@ -225,8 +264,12 @@ class SplitLaunch:
         self.out, self.device = first.out, first.device
         a = _lib.PaSplitArgs()
         a.first, a.second = ctypes.pointer(first.args), ctypes.pointer(second.args)
-        a.run_steps, a.run_start, a.run_groups = _lib.ptr(sched.run), _lib.ptr(sched.start), sched.groups
-        a.kv_bits = _lib.ptr(pool)
+        if isinstance(sched, SplitGrid):
+            self.kernel = "split-grid"
+            a.items, a.n_items = _lib.ptr(sched.items), sched.n_items
+        else:
+            a.run_steps, a.run_start, a.run_groups = _lib.ptr(sched.run), _lib.ptr(sched.start), sched.groups
+            a.kv_bits = _lib.ptr(pool)
         a.sync, a.sync_groups = _lib.ptr(sched.sync), sched.sync_groups
         a.sync_signal, a.sync_wait = sched.sync_signal, sched.sync_wait
         a.status = _lib.ptr(sched.status)

@@ -102,7 +102,8 @@ def test_persistent_split_with_empty_lists_and_merge(gpu):
     # two persistent launches, and one split launch (both pieces in the identity basis:
     # every sync group is one query block of each piece)
     for plan, kinds in ((SplitPlan(pieces, N, gpu, persistent=True, fuse=False), ["run", "run"]),
-                        (SplitPlan(pieces, N, gpu, persistent=True), ["split"])):
+                        (SplitPlan(pieces, N, gpu, persistent=True, fuse=True), ["split"]),
+                        (SplitPlan(pieces, N, gpu, fuse=True), ["split-grid"])):
         launches, _, _ = plan.prepare(qd, kd, vd)
         assert [x.kernel for x in launches] == kinds
         o_r = plan.forward(qd, kd, vd)
@@ -130,7 +131,7 @@ def test_workloads_persistent_equal_per_block(gpu, name):
 
 
 def _split_plans(pieces, N, dev, **kw):
-    fused = SplitPlan(pieces, N, dev, persistent=True, **kw)
+    fused = SplitPlan(pieces, N, dev, persistent=True, fuse=True, **kw)
     two = SplitPlan(pieces, N, dev, persistent=True, fuse=False)
     return fused, two
 
@@ -169,7 +170,7 @@ def test_split_launch_headline_equals_per_block(gpu):
     """At the headline size the one-launch split reproduces the per-block kernels bit for bit."""
     wl = workloads.make("bandlat-L16k")
     q, k, v = wl.inputs(0, gpu)
-    fused = SplitPlan(wl.pieces, wl.L, gpu, persistent=True)
+    fused = SplitPlan(wl.pieces, wl.L, gpu, persistent=True, fuse=True)
     blk = SplitPlan(wl.pieces, wl.L, gpu, persistent=False)
     launches, _, _ = fused.prepare(q, k, v)
     assert [x.kernel for x in launches] == ["split"]
@@ -180,3 +181,49 @@ def test_split_launch_headline_equals_per_block(gpu):
     torch.cuda.synchronize()
     fused.check()
     assert torch.equal(o_f, o_b) and torch.equal(lse_f, lse_b)
+
+
+@pytest.mark.parametrize("N,BH,lag", [(4096, 8, 1), (8192, 3, 0), (4096, 16, 2)])
+def test_split_grid_equals_two_launches(gpu, N, BH, lag):
+    """Both pieces of the band + lattice split as one work-group per item (the lattice
+    merges waiting for the band items of their group) give the per-block two-launch result
+    bit for bit, over repeated launches; the counters are left zero and no wait gave up."""
+    band = pm.SlidingWindow(256)
+    lat = pm.Difference(pm.Dilated(16), band)
+    pieces = [Piece(band, 128, 32), Piece(lat, 128, 32, residue=16)]
+    q, k, v = make_qkv(BH, N, 128, torch.bfloat16, seed=N + BH + lag)
+    qd, kd, vd = (x.to(gpu) for x in (q, k, v))
+    grid = SplitPlan(pieces, N, gpu, fuse=True, split_lag=lag)
+    blk = SplitPlan(pieces, N, gpu)
+    launches, _, _ = grid.prepare(qd, kd, vd)
+    assert [x.kernel for x in launches] == ["split-grid"]
+    lse_g = torch.empty(BH, N, device=gpu)
+    lse_b = torch.empty(BH, N, device=gpu)
+    for _ in range(3):
+        o_g = grid.forward(qd, kd, vd, lse=lse_g)
+    o_b = blk.forward(qd, kd, vd, lse=lse_b)
+    torch.cuda.synchronize()
+    grid.check()
+    sg = grid._runs[("grid", BH)]
+    assert int(sg.sync.abs().sum()) == 0 and int(sg.status.item()) == 0
+    assert torch.equal(o_g, o_b), f"max diff {(o_g.float() - o_b.float()).abs().max().item():.3e}"
+    assert torch.equal(lse_g, lse_b)
+    want, _ = oatt.dense_attention(as64(q), as64(k), as64(v), oatt.spec_rows(om.NAMED["band256+lat16"], N))
+    check_close(o_g, want, torch.bfloat16, "split grid")
+
+
+def test_split_grid_headline_equals_per_block(gpu):
+    """At the headline size the split grid reproduces the per-block kernels bit for bit."""
+    wl = workloads.make("bandlat-L16k")
+    q, k, v = wl.inputs(0, gpu)
+    grid = SplitPlan(wl.pieces, wl.L, gpu, fuse=True)
+    blk = SplitPlan(wl.pieces, wl.L, gpu)
+    launches, _, _ = grid.prepare(q, k, v)
+    assert [x.kernel for x in launches] == ["split-grid"]
+    lse_g = torch.empty(wl.H, wl.L, device=gpu)
+    lse_b = torch.empty(wl.H, wl.L, device=gpu)
+    o_g = grid.forward(q, k, v, lse=lse_g)
+    o_b = blk.forward(q, k, v, lse=lse_b)
+    torch.cuda.synchronize()
+    grid.check()
+    assert torch.equal(o_g, o_b) and torch.equal(lse_g, lse_b)

@@ -107,3 +107,45 @@ def test_split_lists_cover_every_item_in_order_without_cycles(BH, groups, xcds):
         _simulate(lists, speed)
     ideal = (len0.sum() + len1.sum()) * BH / groups
     assert _simulate(lists, np.ones(groups)) < 1.25 * ideal + len1.max()
+
+
+@pytest.mark.parametrize("BH,lag", [(32, 1), (8, 0), (16, 2), (3, 1), (5, 0)])
+def test_split_grid_items_start_after_what_they_wait_for(BH, lag):
+    """One work-group per item: every item exactly once, each head's items on one XCD when
+    the heads split evenly over the XCDs, and every merge starts (work-group id order)
+    after all the first-piece items of its group."""
+    from polyhedral_amd.schedule import XCDS, block_rows, grid_start_order, split_grid_items, sync_groups
+    N = 16384
+    g0, g1, ng = sync_groups(N // 128, lambda p, qb: block_rows(qb, (0, 16)[p], N))
+    len0 = np.full(128, 6)
+    len0[:2] = (2, 4)
+    len1 = 2 * (np.arange(128) % 8) + 2
+    items = split_grid_items(len0, len1, g0, g1, ng, BH, lag=lag)
+    want = {(0, h, q, h * ng + g0[q]) for h in range(BH) for q in range(128)} | \
+           {(1, h, q, h * ng + g1[q]) for h in range(BH) for q in range(128)}
+    assert items.shape == (2 * 128 * BH, 4) and set(map(tuple, items.tolist())) == want
+    hw = grid_start_order(items.shape[0])
+    assert np.array_equal(np.sort(hw), np.arange(items.shape[0]))
+    last_first = {}
+    for (pc, bh, qb, sg), i in zip(items.tolist(), hw.tolist()):
+        if pc == 0:
+            last_first[sg] = max(last_first.get(sg, -1), i)
+    for (pc, bh, qb, sg), i in zip(items.tolist(), hw.tolist()):
+        if pc == 1:
+            assert i > last_first[sg]
+    if BH % XCDS == 0:
+        xcd_of_head = {}
+        for (pc, bh, qb, sg), i in zip(items.tolist(), hw.tolist()):
+            assert xcd_of_head.setdefault(bh, i % XCDS) == i % XCDS
+
+
+def test_grid_start_order_inverts_the_kernel_mapping():
+    """grid_start_order(n)[item] is the work-group that takes the item."""
+    from polyhedral_amd.schedule import XCDS, grid_start_order
+    for n in (1, 7, 8, 9, 64, 1003):
+        per, rem = divmod(n, XCDS)
+        hw = grid_start_order(n)
+        for i in range(n):
+            x, r = i % XCDS, i // XCDS
+            lid = x * per + min(x, rem) + r if r < per else x * per + x + per
+            assert hw[lid] == i
