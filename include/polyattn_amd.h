@@ -348,6 +348,16 @@ typedef struct pa_decode_args {
 int pa_decode_workspace(const pa_decode_args* args, int64_t* bytes);
 int pa_decode_fwd(const pa_decode_args* args, void* stream);
 
+/* pa_decode_fwd_static: pa_decode_fwd that allocates nothing and takes no workspace
+ * (args->workspace NULL, workspace_bytes 0).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops
+ * and harnesses that forbid hipMalloc).  The split partials go to an 8 MiB scratch array
+ * of the library, one per GPU, held until the process ends; a call whose partials need
+ * more (pa_decode_workspace's size) fails with PA_E_INVALID.  Every call on a GPU shares
+ * that GPU's scratch: calls that overlap on one GPU (other streams, other threads) race
+ * and give wrong results; calls in one stream are ordered and safe. */
+int pa_decode_fwd_static(const pa_decode_args* args, void* stream);
+
 /* ---- backward (the reference has none: gpu/triton_attn.py:9-10, README.md:118) ------
  * pa_index_transpose: for each of the nk key blocks, the query blocks whose list
  * (kv_idx / kv_num / kv_partial of an index built at BQ = A, pitch columns) holds it, in

@@ -14,7 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libpolyattn_amd.s
 PA_OK, PA_E_INVALID, PA_E_HIP, PA_E_UNSUPPORTED = 0, -1, -2, -3
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 MAX_TERMS = 8
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -98,6 +98,7 @@ SIGNATURES = {
                                     c_i64, c_i64, c_i32, c_vp]),
     "pa_decode_workspace": (ctypes.c_int, [ctypes.POINTER(PaDecodeArgs), ctypes.POINTER(c_i64)]),
     "pa_decode_fwd": (ctypes.c_int, [ctypes.POINTER(PaDecodeArgs), c_vp]),
+    "pa_decode_fwd_static": (ctypes.c_int, [ctypes.POINTER(PaDecodeArgs), c_vp]),
     "pa_index_transpose": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i32, c_i64, c_i32, c_vp, c_vp, c_vp, c_vp, c_i64,
                                           c_vp]),
     "pa_index_bits_transpose": (ctypes.c_int, [c_vp, c_i32, c_i64, c_vp, c_vp, c_vp]),

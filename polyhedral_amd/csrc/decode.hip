@@ -18,6 +18,8 @@
 // either basis; what the relabelling saves is the visits to blocks with few live keys.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.hpp"
 
 namespace pa {
@@ -446,6 +448,45 @@ extern "C" int pa_decode_workspace(const pa_decode_args* x, int64_t* bytes) {
   return PA_OK;
 }
 
+// The partials of one pa_decode_fwd_static call: a per-device global of the library, so
+// the call allocates nothing.  Host code never passes `scratch` itself (on the host the
+// name is only a stand-in for the symbol): its device address on the current device
+// comes from hipGetSymbolAddress, once per device, in decode_scratch.
+constexpr int64_t kDecodeScratchBytes = 8ll << 20;
+static __device__ __align__(256) float scratch[kDecodeScratchBytes / 4];
+
+namespace pa {
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kScratchDevices] = {};
+
+// The device address of `scratch` on the current device (looked up on the first call
+// on that device, then kept).
+int decode_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  PA_CHECK_ARG(dev >= 0 && dev < kScratchDevices, "pa_decode_fwd_static: device %d beyond %d", dev,
+               kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    PA_CHECK_ARG(ptr != nullptr, "pa_decode_fwd_static: no device address for the scratch array");
+    g_scratch[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return PA_OK;
+}
+
+int decode_launch(const pa_decode_args* x, const Plan& p, float* ws, hipStream_t s);
+
+}  // namespace
+}  // namespace pa
+
 extern "C" int pa_decode_fwd(const pa_decode_args* x, void* stream) {
   const int rc = pa::check_decode(x);
   if (rc) return rc;
@@ -455,7 +496,31 @@ extern "C" int pa_decode_fwd(const pa_decode_args* x, void* stream) {
                                   (reinterpret_cast<uintptr_t>(x->workspace) % 16) == 0),
                "pa_decode_fwd: workspace of %lld bytes (16-byte aligned) needed, got %lld", (long long)need,
                (long long)x->workspace_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  return pa::decode_launch(x, p, static_cast<float*>(x->workspace), static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pa_decode_fwd_static(const pa_decode_args* x, void* stream) {
+  const int rc = pa::check_decode(x);
+  if (rc) return rc;
+  PA_CHECK_ARG(!x->workspace && x->workspace_bytes == 0,
+               "pa_decode_fwd_static: takes no workspace (the partials go to the library's scratch)");
+  const pa::Plan p = pa::plan_of(x->BH, x->capacity, x->length, x->residue_s);
+  const int64_t need = x->BH * (int64_t)p.n_split * x->nq * (x->D + 1) * 4;
+  PA_CHECK_ARG(need <= kDecodeScratchBytes,
+               "pa_decode_fwd_static: the split partials need %lld bytes, more than the %lld-byte scratch "
+               "(call pa_decode_fwd with a workspace)",
+               (long long)need, (long long)kDecodeScratchBytes);
+  float* ws = nullptr;
+  if (p.n_split > 0) {
+    if (int r = pa::decode_scratch(&ws)) return r;
+  }
+  return pa::decode_launch(x, p, ws, static_cast<hipStream_t>(stream));
+}
+
+namespace pa {
+namespace {
+
+int decode_launch(const pa_decode_args* x, const Plan& p, float* ws, hipStream_t s) {
   pa::DecK k;
   k.q = static_cast<const char*>(x->q);
   k.q_sb = x->q_sb;
@@ -474,7 +539,6 @@ extern "C" int pa_decode_fwd(const pa_decode_args* x, void* stream) {
   k.n_split = p.n_split;
   k.c = (x->scale > 0.f ? x->scale : 1.f / sqrtf((float)x->D)) * 1.4426950408889634f;
   k.pred = pa::make_pred(x->mask);
-  float* ws = static_cast<float*>(x->workspace);
   k.o_part = ws;
   k.lse_part = ws ? ws + x->BH * (int64_t)p.n_split * x->nq * x->D : nullptr;
   if (p.n_split > 0) {
@@ -502,6 +566,9 @@ extern "C" int pa_decode_fwd(const pa_decode_args* x, void* stream) {
   PA_LAUNCH_CHECK("decode_merge_kernel");
   return PA_OK;
 }
+
+}  // namespace
+}  // namespace pa
 
 extern "C" int pa_kv_append(const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sn, void* k_cache,
                             void* v_cache, int64_t c_sb, int64_t c_sn, int64_t BH, int64_t n, int32_t D,

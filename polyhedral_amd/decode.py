@@ -35,15 +35,18 @@ def _rows_ok(t, name):
 
 
 class DecodeLaunch:
-    """A validated pa_decode_fwd call with its workspace; __call__ launches it on the
-    current stream of its device and returns the output."""
+    """A validated pa_decode_fwd call with its workspace (or a pa_decode_fwd_static call,
+    which uses the library's scratch); __call__ launches it on the current stream of its
+    device and returns the output."""
 
-    def __init__(self, args, keep, out, device):
+    def __init__(self, args, keep, out, device, static_scratch=False):
         self.args, self.keep, self.out, self.device = args, keep, out, device
+        self.entry = "pa_decode_fwd_static" if static_scratch else "pa_decode_fwd"
+        self._fn = getattr(_lib.lib(), self.entry)
         self._ref = ctypes.byref(args)
 
     def __call__(self):
-        _lib.check(_lib.lib().pa_decode_fwd(self._ref, _lib.stream_of(self.out)), "pa_decode_fwd")
+        _lib.check(self._fn(self._ref, _lib.stream_of(self.out)), self.entry)
         return self.out
 
 
@@ -91,11 +94,14 @@ class KVCache:
                 self.capacity, self.length, self.residue, _lib.stream_of(self.k)), "pa_kv_append")
         self.length += n
 
-    def prepare(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None):
+    def prepare(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None, static_scratch=False):
         """A DecodeLaunch of q [BH, nq, D] (nq <= 8, queries at original positions qpos0 ..
         qpos0 + nq - 1, by default the last nq tokens) against the first ``length`` cached
         tokens (default: all).  mask: a polyattn mask object, a MaskSpec or a DeviceMask
-        without permutation tables; the cache's basis is applied by the kernel."""
+        without permutation tables; the cache's basis is applied by the kernel.
+        static_scratch: launch pa_decode_fwd_static, which allocates nothing (its split
+        partials go to the library's 8 MiB per-GPU scratch; launches that overlap on one
+        GPU race)."""
         _lib.require_device(q)
         _rows_ok(q, "q")
         BH, nq, D = q.shape
@@ -131,14 +137,16 @@ class KVCache:
             if lse.dtype != torch.float32 or lse.shape != (BH, nq) or lse.stride(1) != 1:
                 raise ValueError("lse must be float32 [BH, nq] with unit stride")
             a.lse, a.lse_sb = _lib.ptr(lse), lse.stride(0)
+        if static_scratch:
+            return DecodeLaunch(a, [q, o, lse, dm, self.k, self.v], o, dev, static_scratch=True)
         nbytes = ctypes.c_int64(0)
         _lib.check(_lib.lib().pa_decode_workspace(ctypes.byref(a), ctypes.byref(nbytes)), "pa_decode_workspace")
         ws = torch.empty(max(1, (nbytes.value + 3) // 4), dtype=torch.float32, device=dev)
         a.workspace, a.workspace_bytes = _lib.ptr(ws), ws.numel() * 4
         return DecodeLaunch(a, [q, o, lse, dm, ws, self.k, self.v], o, dev)
 
-    def attend(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None):
+    def attend(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None, static_scratch=False):
         """o [BH, nq, D]: see prepare."""
-        launch = self.prepare(q, mask, scale, qpos0, out, lse, length)
+        launch = self.prepare(q, mask, scale, qpos0, out, lse, length, static_scratch)
         with torch.cuda.device(self.device):
             return launch()

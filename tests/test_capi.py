@@ -201,3 +201,26 @@ def test_decode_rejects_more_residue_classes_than_the_merge_takes():
     from polyhedral_amd import decode as pdec
     with pytest.raises(ValueError):
         pdec.KVCache(1, 16384, 128, residue=8192, device="cpu")
+
+
+def test_static_decode_rejects_a_workspace_and_partials_beyond_its_scratch():
+    """pa_decode_fwd_static takes no workspace, and refuses (before touching a device) a
+    call whose split partials exceed its 8 MiB scratch."""
+    lib = _lib.lib()
+    a = _lib.PaDecodeArgs()
+    buf = (ctypes.c_int64 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    a.q, a.k_cache, a.v_cache, a.o = p, p, p, p
+    a.nq, a.BH, a.D, a.dtype = 8, 4096, 128, _lib.PA_BF16
+    a.q_sb, a.q_sn, a.c_sb, a.c_sn, a.o_sb, a.o_sn = 1024, 128, 256 * 128, 128, 1024, 128
+    a.capacity, a.length, a.residue_s = 256, 256, 0
+    a.mask.n_include = 1
+    n = ctypes.c_int64(0)
+    assert lib.pa_decode_workspace(ctypes.byref(a), ctypes.byref(n)) == _lib.PA_OK
+    assert n.value == 4096 * 8 * 129 * 4 > 8 << 20
+    assert lib.pa_decode_fwd_static(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"scratch" in lib.pa_last_error()
+    a.BH = 1
+    a.workspace, a.workspace_bytes = p, 512
+    assert lib.pa_decode_fwd_static(ctypes.byref(a), None) == _lib.PA_E_INVALID
+    assert b"takes no workspace" in lib.pa_last_error()
