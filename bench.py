@@ -448,7 +448,8 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0", extra
     backward = (measure_backward(wl, q, k, v, o, lse, max(residues) if residues else 0)
                 if extras and wl.D in (64, 128) and wl.dtype != torch.float32 and wl.L % 64 == 0 else None)
     kernels = [{"run": "attn_run_kernel", "split": "attn_run_kernel (split)", "stream": "attn_stream_kernel",
-                "split-grid": "attn_stream_kernel (split)"}.get(x.kernel, "attn_fwd_kernel") for x in launches]
+                "split-grid": "attn_stream_kernel (split)", "wsplit": "attn_wsplit_kernel"}.get(x.kernel, "attn_fwd_kernel")
+               for x in launches]
     per = [0.0] * len(plan.built)       # per piece; an empty piece has no launch
     piece_kernel = [None] * len(plan.built)
     for i, pcs in enumerate(plan.launched):

@@ -246,6 +246,14 @@ typedef struct pa_attn_args {
   const int32_t* run_steps;
   const int32_t* run_start;   /* [run_groups + 1] */
   int32_t run_groups;
+  /* wave_split != 0: the wave-split kernel (no counterpart in the reference), for grids
+   * too small to fill the chip: one 8-wave work-group per (batch-head, 16 query rows),
+   * the waves splitting the rows' live 16x16 sub-tiles and merging their softmax states
+   * in LDS.  float32, D = 64 or 128, BQ and A multiples of 32, kv_wave_bits given, no
+   * permutation (perm tables, gathers, scatter, residue basis), no class-B emulation, no
+   * prev_o, no kv_steps / run_groups; results within float32 rounding of the general
+   * kernel's. */
+  int32_t wave_split;
 } pa_attn_args;
 
 int pa_attn_fwd(const pa_attn_args* args, void* stream);

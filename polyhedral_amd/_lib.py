@@ -14,7 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libpolyattn_amd.s
 PA_OK, PA_E_INVALID, PA_E_HIP, PA_E_UNSUPPORTED = 0, -1, -2, -3
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 MAX_TERMS = 8
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -42,7 +42,8 @@ class PaAttnArgs(ctypes.Structure):
                 ("prev_o", c_vp), ("prev_dtype", c_i32), ("prev_sb", c_i64), ("prev_sn", c_i64),
                 ("prev_lse", c_vp), ("qblock_order", c_vp), ("kv_steps", c_vp), ("steps_pitch", c_i64),
                 ("heads_desc", c_i32), ("gather_mult", c_i32), ("gather_scatter", c_i32), ("wsel", c_vp),
-                ("wsel_sb", c_i64), ("run_steps", c_vp), ("run_start", c_vp), ("run_groups", c_i32)]
+                ("wsel_sb", c_i64), ("run_steps", c_vp), ("run_start", c_vp), ("run_groups", c_i32),
+                ("wave_split", c_i32)]
 
 
 class PaSplitArgs(ctypes.Structure):

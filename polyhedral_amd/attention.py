@@ -65,13 +65,19 @@ def _rows3(t, name):
     return t
 
 
+# below this many (batch-head, query block) work-groups the general kernel leaves CUs idle
+# (MI355X: 256 CUs), and float32 calls go to the wave-split kernel (one work-group per 16
+# query rows)
+WSPLIT_MAX_BLOCKS = 256
+
+
 class Launch:
     """A validated pa_attn_fwd argument block and the tensors its pointers refer to.
     __call__ launches it on the current stream of its device (no re-validation)."""
 
     def __init__(self, args, keep, out, device, kernel):
         self.args, self.keep, self.out, self.device = args, keep, out, device
-        self.kernel = kernel  # "run", "stream" or "general"
+        self.kernel = kernel  # "run", "stream", "wsplit" or "general"
         self._ref = ctypes.byref(args)
 
     def __call__(self):
@@ -135,11 +141,11 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
         kv_wave_bits = kv_wave_bits.to(torch.int32).contiguous()
         if kv_wave_bits.shape != kv_idx.shape:
             raise ValueError("kv_wave_bits must have the shape of kv_idx")
-    if kernel not in ("auto", "stream", "general"):
-        raise ValueError(f"kernel={kernel!r}: expected 'auto', 'stream' or 'general'")
+    if kernel not in ("auto", "stream", "general", "wsplit"):
+        raise ValueError(f"kernel={kernel!r}: expected 'auto', 'stream', 'general' or 'wsplit'")
     # the K / V rows of the step descriptors are in the basis K / V are gathered through
     steps_basis = int(residue) if (gather_kv and residue) else 0
-    if kernel != "general" and (kv_bits is None or kv_steps is None):
+    if kernel not in ("general", "wsplit") and (kv_bits is None or kv_steps is None):
         reg_bits, reg_steps = stream_arrays_for(kv_idx, BQ, A, steps_basis, qblock_order)
         if kv_bits is None and kv_steps is None:
             kv_bits = reg_bits
@@ -236,7 +242,7 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
         why = "no step descriptors for this index"
     if kernel == "stream" and why is not None:
         raise ValueError(f"the streaming kernel cannot take this call: {why}")
-    use_stream = kernel != "general" and why is None and pitch > 0
+    use_stream = kernel not in ("general", "wsplit") and why is None and pitch > 0
     if use_stream:
         _lib.require_device(kv_steps)
         if kv_steps.dtype != torch.int32 or kv_steps.dim() != 3 or kv_steps.shape[0] != nq \
@@ -254,6 +260,23 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
             if t.stride(0) != N * t.stride(1):
                 raise ValueError(f"the persistent kernel needs {n} with batch stride N * row stride")
         args.run_steps, args.run_start, args.run_groups = _lib.ptr(run.run), _lib.ptr(run.start), run.groups
+    # the wave-split kernel (pa_attn_args.wave_split): float32 grids of fewer query blocks
+    # than the chip has CUs, where one work-group per block would leave most of it idle
+    why_ws = None
+    if q.dtype != torch.float32 or D not in (64, 128) or BQ % 32 or A % 32:
+        why_ws = f"dtype {q.dtype}, D={D}, tile {BQ}x{A} (needs float32, D = 64 or 128, BQ and A multiples of 32)"
+    elif kv_wave_bits is None and kv_idx.shape[1] > 0:
+        why_ws = "no wave-group codes for this index"
+    elif (dmask.perm_q is not None or dmask.perm_kv is not None or gather_q or gathers_kv or scatter_o
+          or residue):
+        why_ws = "a permutation"
+    elif gather_mult > 1 or prev is not None:
+        why_ws = "class-B emulation or a merge input"
+    if kernel == "wsplit" and why_ws is not None:
+        raise ValueError(f"the wave-split kernel cannot take this call: {why_ws}")
+    use_ws = (not use_stream and why_ws is None and
+              (kernel == "wsplit" or (kernel == "auto" and BH * nq < WSPLIT_MAX_BLOCKS)))
+    args.wave_split = 1 if use_ws else 0
     args.heads_desc = 1 if heads_desc else 0
     wsel_t = None
     if gather_mult > 1:
@@ -270,4 +293,5 @@ def prepare(q, k, v, kv_idx, kv_num, kv_partial, kind, p0, p1, p2, BQ, A, scale=
         args.wsel, args.wsel_sb = _lib.ptr(wsel_t), wsel_t.stride(0)
     keep = [q, k, v, o, kv_idx, kv_num, kv_partial, kv_wave_bits, kv_bits, dmask, lse, prev, qblock_order,
             kv_steps, wsel_t, run]
-    return Launch(args, keep, o, dev, "run" if use_run else "stream" if use_stream else "general")
+    return Launch(args, keep, o, dev,
+                  "run" if use_run else "stream" if use_stream else "wsplit" if use_ws else "general")

@@ -21,7 +21,7 @@ LIB = LIBDIR / "libpolyattn_amd.so"
 ARCH = "gfx950"
 
 SOURCES = ["common.hip", "index.hip", "permute.hip", "merge.hip", "attn_fwd.hip",
-           "attn_bf16.hip", "attn_f16.hip", "attn_f32.hip", "attn_stream.hip", "decode.hip", "bwd.hip"]
+           "attn_bf16.hip", "attn_f16.hip", "attn_f32.hip", "attn_stream.hip", "attn_wsplit.hip", "decode.hip", "bwd.hip"]
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-mcode-object-version=5",

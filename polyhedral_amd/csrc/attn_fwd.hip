@@ -8,6 +8,7 @@ namespace pa {
 int launch_attn_bf16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f16(const AttnK& a, int D, int NW, hipStream_t s);
 int launch_attn_f32(const AttnK& a, int D, int NW, hipStream_t s);
+int launch_attn_wsplit(const AttnK& a, int D, hipStream_t s);
 int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s);
 int launch_attn_run(const AttnK& a, int groups, int dtype, bool cooperative, hipStream_t s);
 int launch_attn_split_grid(const AttnK& a, int dtype, hipStream_t s);
@@ -151,6 +152,20 @@ extern "C" int pa_attn_fwd(const pa_attn_args* x, void* stream) {
   const int NW = x->BQ >= 32 ? x->BQ / 32 : 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (x->run_groups > 0) return pa::launch_attn_run(a, x->run_groups, x->dtype, false, s);
+  if (x->wave_split) {
+    // the wave-split kernel: asked for explicitly, so its preconditions are errors
+    PA_CHECK_ARG(x->dtype == PA_F32 && (x->D == 64 || x->D == 128),
+                 "pa_attn_fwd: wave_split needs float32 with D = 64 or 128");
+    PA_CHECK_ARG(x->BQ % 32 == 0 && x->A % 32 == 0, "pa_attn_fwd: wave_split needs BQ and A multiples of 32");
+    PA_CHECK_ARG(x->kv_wave_bits || x->pitch == 0, "pa_attn_fwd: wave_split needs kv_wave_bits");
+    PA_CHECK_ARG(!x->gather_q && !x->gather_kv && !x->scatter_o && x->residue_s <= 0 && !x->mask.perm_q &&
+                     !x->mask.perm_kv,
+                 "pa_attn_fwd: wave_split takes no permutation");
+    PA_CHECK_ARG(x->gather_mult <= 1 && !x->prev_o && !x->kv_steps,
+                 "pa_attn_fwd: wave_split takes no class-B emulation, prev_o or kv_steps");
+    PA_CHECK_ARG(x->BH * (x->N / 16) < (1ll << 31), "pa_attn_fwd: wave_split grid too large");
+    return pa::launch_attn_wsplit(a, x->D, s);
+  }
   if (x->kv_steps) {
     // the streaming kernel: asked for by passing the step descriptors, so its
     // preconditions are errors rather than a silent change of kernel
