@@ -98,6 +98,7 @@ void attn_stream_kernel(const AttnK a) {
   typedef const __attribute__((address_space(4))) int32_t cint;
   int64_t bh;
   int pc = 0, sg = -1;
+  int qb_direct;  // the query block when it is known without reading the first descriptor
   const StepDesc* desc;
   if constexpr (SPLIT) {
     // the item of this work-group and its piece's descriptors (index order)
@@ -106,6 +107,7 @@ void attn_stream_kernel(const AttnK a) {
     bh = it[1];
     sg = it[3];
     desc = reinterpret_cast<const StepDesc*>(pc ? a.steps1 : a.steps) + (int64_t)it[2] * (pc ? a.steps_pitch1 : a.steps_pitch);
+    qb_direct = it[2];
   } else {
     const uint32_t bh_l = lid / (uint32_t)a.nq;
     bh = a.heads_desc ? a.BH - 1 - bh_l : bh_l;
@@ -113,8 +115,11 @@ void attn_stream_kernel(const AttnK a) {
     // The lists are laid out in issue order; a list's first descriptor names its query
     // block and its length, so one scalar load starts the work-group.
     desc = reinterpret_cast<const StepDesc*>(a.steps) + (int64_t)qb_lin * a.steps_pitch;
+    qb_direct = a.qblock_order ? -1 : qb_lin;
   }
-  const int qb = ((cint*)desc)[13];
+  // Lists in index order (a split grid's, or a launch without an issue order) start on
+  // their own query block, so the query rows' loads need not wait for the descriptor.
+  const int qb = qb_direct >= 0 ? qb_direct : ((cint*)desc)[13];
   const int n_steps = ((cint*)desc)[14];
   const int A = a.A;
 
