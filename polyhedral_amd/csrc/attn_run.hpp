@@ -154,6 +154,30 @@ void attn_run_kernel(const AttnK a) {
     r.pad[2] = c[11];  // sync group
     return r;
   };
+  // Inside the step loop a run row is one vector load (lane l reads word l % 16), unpacked
+  // with v_readlane after the next iteration's vmcnt(0) wait: a scalar load there would
+  // share lgkmcnt with the LDS reads of the MFMA block and, returning out of order, make
+  // its first LDS wait an lgkmcnt(0) that stalls on the row (a miss: each row is read once).
+  const int lane16 = lane & 15;
+  auto load_desc_v = [&](int jd) __attribute__((always_inline)) -> int32_t {
+    return reinterpret_cast<const int32_t*>(desc + jd)[lane16];
+  };
+  auto unpack_desc = [&](int32_t dv) __attribute__((always_inline)) -> StepDesc {
+    StepDesc r{};
+    r.base[0] = __builtin_amdgcn_readlane(dv, 0);
+    r.base[1] = __builtin_amdgcn_readlane(dv, 1);
+    r.base[2] = __builtin_amdgcn_readlane(dv, 2);
+    r.base[3] = __builtin_amdgcn_readlane(dv, 3);
+    r.code = (uint32_t)__builtin_amdgcn_readlane(dv, 4);
+    r.boff[0] = __builtin_amdgcn_readlane(dv, 5);
+    r.boff[1] = __builtin_amdgcn_readlane(dv, 6);
+    r.boff[2] = __builtin_amdgcn_readlane(dv, 7);
+    r.boff[3] = __builtin_amdgcn_readlane(dv, 8);
+    r.pad[0] = __builtin_amdgcn_readlane(dv, 9);
+    r.pad[1] = __builtin_amdgcn_readlane(dv, 10);
+    r.pad[2] = __builtin_amdgcn_readlane(dv, 11);
+    return r;
+  };
   struct Flags {
     uint32_t live, full;
   };
@@ -321,6 +345,7 @@ void attn_run_kernel(const AttnK a) {
     _Pragma("unroll") for (int kc = 0; kc < NQF; ++kc) asm volatile("" ::"v"(qf[kc]));             \
     __syncthreads();                                                                              \
     if ((jj) + 2 < n_steps) {                                                                     \
+      d_j2 = unpack_desc(dv_j2);                                                                  \
       const uint32_t k_goff = (d_j2.pad[0] & kRunPiece) ? k_goff1 : k_goff0;                      \
       PA_DMA_K(d_j2, (P));                                                                        \
     }                                                                                             \
@@ -328,8 +353,7 @@ void attn_run_kernel(const AttnK a) {
       const uint32_t v_goff = (d_j1.pad[0] & kRunPiece) ? v_goff1 : v_goff0;                      \
       PA_DMA_V(d_j1, (P) ^ 1);                                                                    \
     }                                                                                             \
-    StepDesc d_j3{};                                                                              \
-    if ((jj) + 3 < n_steps) d_j3 = load_desc((jj) + 3);                                           \
+    if ((jj) + 3 < n_steps) dv_j2 = load_desc_v((jj) + 3);                                        \
     const Flags fn = flags_of(d_j1.code);                                                         \
     const int fl_n = d_j1.pad[0];                                                                 \
     const float neg_m = -m_run;                                                                   \
@@ -368,7 +392,6 @@ void attn_run_kernel(const AttnK a) {
     fc = fn;                                                                                      \
     fl_c = fl_n;                                                                                  \
     d_j1 = d_j2;                                                                                  \
-    d_j2 = d_j3;                                                                                  \
   } while (0)
 
   // The last step of the run: its V (slot P) arrives, then its softmax and P.V.
@@ -392,7 +415,10 @@ void attn_run_kernel(const AttnK a) {
 
   // Prologue: the first item's Q, step 0's K, bitmaps and V, then step 1's K; QK, shaping
   // and maximum of step 0.
+  // d_j1 / d_j2: run rows of the steps one and two ahead; dv_j2: the raw row (one word per
+  // lane) that becomes d_j2 at the top of the next iteration
   StepDesc d_j1{}, d_j2{};
+  int32_t dv_j2 = 0;
   Flags fc{0u, 0u};
   int fl_c;
   int cur_bh, cur_qb, cur_sg;
@@ -400,7 +426,7 @@ void attn_run_kernel(const AttnK a) {
   {
     const StepDesc d0 = load_desc(0);
     if (n_steps > 1) d_j1 = load_desc(1);
-    if (n_steps > 2) d_j2 = load_desc(2);
+    if (n_steps > 2) dv_j2 = load_desc_v(2);
     cur_bh = d0.pad[1];
     cur_qb = d0.pad[0] >> kRunQbShift;
     cur_sg = d0.pad[2];

@@ -215,9 +215,12 @@ void attn_stream_kernel(const AttnK a) {
   float l_part = 0.f;
   const float cexp = a.c;
 
-  // Descriptors are read through the constant address space: the kernel never writes
-  // them, and that lets the compiler use scalar loads (a vector load would be counted
-  // in vmcnt together with the DMA and make the compiler's waits cover it).
+  // The first descriptors of a list are read through the constant address space, as
+  // scalar loads.  Inside the step loop a descriptor is instead one vector load (lane l
+  // reads word l % 16), unpacked with v_readlane after the next iteration's vmcnt(0)
+  // wait, which the DMA needs anyway: a scalar load there would share lgkmcnt with the
+  // LDS reads, and since scalar loads return out of order, the first LDS wait of the
+  // MFMA block would have to be lgkmcnt(0) and would stall on the scalar load.
   auto load_desc = [&](int jd) __attribute__((always_inline)) -> StepDesc {
     cint* c = (cint*)(reinterpret_cast<const int32_t*>(desc + jd));
     StepDesc r{};
@@ -230,6 +233,22 @@ void attn_stream_kernel(const AttnK a) {
     r.boff[1] = c[6];
     r.boff[2] = c[7];
     r.boff[3] = c[8];
+    return r;
+  };
+  auto load_desc_v = [&](int jd) __attribute__((always_inline)) -> int32_t {
+    return reinterpret_cast<const int32_t*>(desc + jd)[lane & 15];
+  };
+  auto unpack_desc = [&](int32_t dv) __attribute__((always_inline)) -> StepDesc {
+    StepDesc r{};
+    r.base[0] = __builtin_amdgcn_readlane(dv, 0);
+    r.base[1] = __builtin_amdgcn_readlane(dv, 1);
+    r.base[2] = __builtin_amdgcn_readlane(dv, 2);
+    r.base[3] = __builtin_amdgcn_readlane(dv, 3);
+    r.code = (uint32_t)__builtin_amdgcn_readlane(dv, 4);
+    r.boff[0] = __builtin_amdgcn_readlane(dv, 5);
+    r.boff[1] = __builtin_amdgcn_readlane(dv, 6);
+    r.boff[2] = __builtin_amdgcn_readlane(dv, 7);
+    r.boff[3] = __builtin_amdgcn_readlane(dv, 8);
     return r;
   };
   // This wave's view of a step: bit t = segment t has a live pair / is all live.
@@ -268,14 +287,14 @@ void attn_stream_kernel(const AttnK a) {
     dma_wait_all();                                                                               \
     __syncthreads();                                                                              \
     if ((jj) + 2 < n_steps) {                                                                     \
+      d_j2 = unpack_desc(dv_j2);                                                                  \
       PA_DMA_K(d_j2, (P));                                                                        \
     } else if (prev_dma) {                                                                        \
       PA_SPLIT_WAIT();                                                                            \
       PA_DMA_PREV(0, (P));                                                                        \
     }                                                                                             \
     PA_DMA_V(d_j1, (P) ^ 1);                                                                      \
-    StepDesc d_j3{};                                                                              \
-    if ((jj) + 3 < n_steps) d_j3 = load_desc((jj) + 3);                                           \
+    if ((jj) + 3 < n_steps) dv_j2 = load_desc_v((jj) + 3);                                        \
     const Flags fn = flags_of(d_j1.code);                                                         \
     const float neg_m = -m_run;                                                                   \
     f32x16 sn0, sn1;                                                                              \
@@ -304,7 +323,6 @@ void attn_stream_kernel(const AttnK a) {
     sc1 = sn1;                                                                                    \
     fc = fn;                                                                                      \
     d_j1 = d_j2;                                                                                  \
-    d_j2 = d_j3;                                                                                  \
   } while (0)
 
   // The last step: its V (slot P) arrives, then its softmax and P.V.  The previous
@@ -388,13 +406,16 @@ void attn_stream_kernel(const AttnK a) {
 
   // Prologue: step 0's K, bitmaps and V; then step 1's K; QK, shaping and maximum of
   // step 0.
+  // d_j1 / d_j2: descriptors of the steps one and two ahead; dv_j2: the raw descriptor
+  // (one word per lane) that becomes d_j2 at the top of the next iteration
   StepDesc d_j1{}, d_j2{};
+  int32_t dv_j2 = 0;
   Flags fc{0u, 0u};
   f32x16 sc0, sc1;
   if (n_steps > 0) {
     const StepDesc d0 = load_desc(0);
     if (n_steps > 1) d_j1 = load_desc(1);
-    if (n_steps > 2) d_j2 = load_desc(2);
+    if (n_steps > 2) dv_j2 = load_desc_v(2);
     PA_DMA_K(d0, 0);
     PA_DMA_V(d0, 0);
     dma_wait_all();
