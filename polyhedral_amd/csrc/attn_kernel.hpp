@@ -223,11 +223,15 @@ __device__ __forceinline__ void dma_x4_sc1(uint32_t m0, const char* gbase, uint3
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 sc1" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
 }
 // A 16-byte agent-scope store (sc1: written through to memory, visible to every XCD once
-// complete); the caller waits for it (s_waitcnt vmcnt) before publishing.
+// complete); the caller waits for it (s_waitcnt vmcnt) before publishing.  On gfx950 a VALU
+// write to the data registers of a store wider than 8 bytes needs two wait states after
+// the store; the compiler's hazard pass does not look inside inline assembly, so the
+// s_nop 1 is part of it (without it the next instruction may overwrite the data before
+// the store has read it).
 __device__ __forceinline__ void store_x4_sc1(char* p, uint32_t x, uint32_t y, uint32_t z, uint32_t w) {
   typedef uint32_t v4 __attribute__((ext_vector_type(4)));
   const v4 v = {x, y, z, w};
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
 }
 
 // Uniform description of the 4 segments (16 index-space KV rows each) of one step.
