@@ -10,7 +10,7 @@
 //
 // pa_kv_append writes the new rows.  pa_decode_fwd attends up to 8 query rows at
 // original positions qpos0 .. qpos0 + nq - 1 to the first `length` tokens under any
-// pa_mask, split over the keys: one work-group per (chunk of one class's segment, head)
+// pa_mask, split over the keys: one work-group per (share of one class's segment, head)
 // writes a normalised partial and its log-sum-exp into the workspace, and a second
 // kernel merges the partials.  Keys are visited in 64-key blocks, one per wave and
 // one key per lane: a block with no live pair is not read at all, and in a block only
@@ -27,7 +27,7 @@ namespace {
 
 constexpr int kDecMaxQ = 8;     // query rows per call
 constexpr int kDecWaves = 4;    // waves per work-group
-constexpr int kDecTarget = 768;    // work-groups a split plan aims for
+constexpr int kDecTarget = 512;    // work-groups a split plan aims for (two per CU, one round)
 constexpr int kMergeMax = 4096;    // splits per (head, query) the merge takes
 
 typedef uint32_t du4 __attribute__((ext_vector_type(4)));
@@ -110,7 +110,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // One work-group per (split, head).  Lane l of wave w scores key b0 + l of each block
-// b0 = i0 + 64 (w + 4 r) from its K row; the V rows of the block's live keys go by LDS
+// b0 = 256 (jc + r per_class) + 64 w from its K row; the V rows of the block's live keys go by LDS
 // DMA into the wave's 64-row buffer, and for P.V the lanes own output dimensions
 // (D / 64 each).  MQ = 1 is the single-query case (fewer registers), MQ = kDecMaxQ
 // takes 2..8 queries.
@@ -144,12 +144,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
   }
   __syncthreads();
 
-  // this split's keys: entries i0 .. i1 - 1 of class cls's segment
+  // this split's keys: the groups of 256 entries jc, jc + per_class, jc + 2 per_class, ...
+  // of class cls's segment (a.chunk = 256 per_class entries apart), one 64-key block per
+  // wave and group, so that a run of live keys is spread over the class's work-groups
   const int cls = split / a.per_class;
   const int64_t jc = split - (int64_t)cls * a.per_class;
   const int64_t cnt = a.length > cls ? (a.length - 1 - cls) / a.s + 1 : 0;
-  const int64_t i0 = jc * a.chunk;
-  const int64_t i1 = cnt < i0 + a.chunk ? cnt : i0 + a.chunk;
+  const int64_t i0 = jc * 256;
+  const int64_t i1 = cnt;
   const char* kseg = a.k + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
   const char* vseg = a.v + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
   const int64_t rowb = a.c_sn * ESZ;
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
     for (int d = 0; d < DPL; ++d) o[i][d] = 0.f;
   }
 
-  for (int64_t b0 = i0 + 64 * w; b0 < i1; b0 += 64 * kDecWaves) {
+  for (int64_t b0 = i0 + 64 * w; b0 < i1; b0 += a.chunk) {
     const int64_t idx = b0 + lane;
     const int32_t t = (int32_t)(idx * a.s + cls);  // original position of this lane's key
     uint32_t lv = 0u;                              // bit i: (query i, key) is live
@@ -374,23 +376,22 @@ struct Plan {
   int64_t chunk, Q;
 };
 
-// Split of the keys: every class's segment in chunks of a multiple of 256 keys (one
-// 64-key block per wave), enough chunks for about kDecTarget work-groups.
+// Split of the keys: per_class work-groups per class's segment, about kDecTarget in all
+// and at most one per 256-key group; work-group j of a class takes groups j, j +
+// per_class, ... (chunk = the stride between them in entries).
 Plan plan_of(int64_t BH, int64_t capacity, int64_t length, int32_t residue_s) {
   Plan p;
   p.s = residue_s > 1 ? residue_s : 1;
   p.Q = capacity / p.s;
   const int64_t cnt_max = (length + p.s - 1) / p.s;
   int64_t per = (kDecTarget + BH * p.s - 1) / (BH * p.s);
+  const int64_t groups = (cnt_max + 255) / 256;
+  if (per > groups) per = groups;
   if (per < 1) per = 1;
-  int64_t chunk = (cnt_max + per - 1) / per;
-  chunk = ((chunk + 255) / 256) * 256;
-  if (chunk < 256) chunk = 256;
-  // the merge holds one weight per split in LDS
-  // (terminates: s <= kMergeMax is checked, and one chunk per class fits once chunk >= cnt_max)
-  while (chunk < cnt_max && p.s * ((cnt_max + chunk - 1) / chunk) > kMergeMax) chunk *= 2;
-  p.chunk = chunk;
-  p.per_class = (int32_t)(cnt_max > 0 ? (cnt_max + chunk - 1) / chunk : 0);
+  // the merge holds one weight per split in LDS (terminates: s <= kMergeMax is checked)
+  while (per > 1 && p.s * per > kMergeMax) per = (per + 1) / 2;
+  p.per_class = (int32_t)(cnt_max > 0 ? per : 0);
+  p.chunk = per * 256;
   p.n_split = p.s * p.per_class;
   return p;
 }
