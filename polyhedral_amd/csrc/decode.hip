@@ -110,9 +110,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // One work-group per (split, head).  Lane l of wave w scores key b0 + l of each block
-// b0 = 256 (jc + r per_class) + 64 w from its K row; the V rows of the block's live keys go by LDS
-// DMA into the wave's 64-row buffer, and for P.V the lanes own output dimensions
-// (D / 64 each).  MQ = 1 is the single-query case (fewer registers), MQ = kDecMaxQ
+// b0 = 256 (jc + r per_class) + 64 w from its K row; the V rows of the block's live keys
+// go by LDS DMA into the wave's 64-row buffer, and for P.V the lanes own output
+// dimensions (D / 64 each).  MQ = 1 is the single-query case (fewer registers), MQ = kDecMaxQ
 // takes 2..8 queries.
 template <typename T, int D, int MQ>
 __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
@@ -223,23 +223,34 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
     // P.V over the live keys, V from the buffer (this wave's own DMA: waiting for it is enough)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const char* vrow = vbuf + w * 64 * RB + lane * DPL * ESZ;
+    // eight keys at a time: their buffer rows are read together (a dead key's row holds
+    // stale data and is read but not used), so the reads' latency is paid once per eight
 #pragma unroll
-    for (int u = 0; u < 64; ++u) {
-      if ((any >> u) & 1ull) {
-        uint32_t vw;
+    for (int u0 = 0; u0 < 64; u0 += 8) {
+      const uint32_t bits8 = (uint32_t)(any >> u0) & 0xffu;
+      if (bits8 == 0u) continue;
+      uint32_t vw[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
         if constexpr (DPL * ESZ == 4)
-          vw = *reinterpret_cast<const uint32_t*>(vrow + u * RB);
+          vw[e] = *reinterpret_cast<const uint32_t*>(vrow + (u0 + e) * RB);
         else
-          vw = *reinterpret_cast<const uint16_t*>(vrow + u * RB);
-        float vx[DPL];
-        vx[0] = Dec<T>::lo(vw);
-        if constexpr (DPL == 2) vx[DPL - 1] = Dec<T>::hi(vw);
+          vw[e] = *reinterpret_cast<const uint16_t*>(vrow + (u0 + e) * RB);
+      }
 #pragma unroll
-        for (int i = 0; i < MQ; ++i) {
-          if (i < nq) {
-            const float pk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), u));
+      for (int e = 0; e < 8; ++e) {
+        if ((bits8 >> e) & 1u) {
+          float vx[DPL];
+          vx[0] = Dec<T>::lo(vw[e]);
+          if constexpr (DPL == 2) vx[DPL - 1] = Dec<T>::hi(vw[e]);
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) o[i][d] = __builtin_fmaf(pk, vx[d], o[i][d]);
+          for (int i = 0; i < MQ; ++i) {
+            if (i < nq) {
+              const float pk =
+                  __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[i]), u0 + e));
+#pragma unroll
+              for (int d = 0; d < DPL; ++d) o[i][d] = __builtin_fmaf(pk, vx[d], o[i][d]);
+            }
           }
         }
       }
