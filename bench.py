@@ -140,11 +140,12 @@ def measure_permute(q, k, v, s, reps=50, warmup=10):
 
 def measure_decode(wl, q, k, v, residues=(0, 16), reps=200, warmup=20):
     """One decode step of the workload's mask against a cache of all L tokens: the newest
-    token's K / V appended (pa_kv_append, rewriting the same row every step) and its query
-    row attended to the cache (pa_decode_fwd, split kernel + merge), captured in a HIP
-    graph and replayed (the step is a few microseconds of kernels; eager launches would
-    time the host).  Algorithmic bytes: the live keys' K and V rows, the appended rows,
-    q and o."""
+    token's K / V appended and its query row attended to the cache, in one pa_decode_fwd
+    call (split kernel + merge; the split's work-group owning the new row writes it,
+    rewriting the same row every step), captured in a HIP graph and replayed (the step is
+    a few microseconds of kernels).  The same step as pa_kv_append then pa_decode_fwd is
+    timed beside it (`separate_ms_per_token`), and both are also timed launched eagerly.
+    Algorithmic bytes: the live keys' K and V rows, the appended rows, q and o."""
     import ctypes
 
     import torch
@@ -157,54 +158,65 @@ def measure_decode(wl, q, k, v, residues=(0, 16), reps=200, warmup=20):
     nbytes = H * (2 * live * rb + 2 * rb + 2 * rb)
     out = {}
     for s in residues:
+        kn, vn, qn = k[:, L - 1:].contiguous(), v[:, L - 1:].contiguous(), q[:, L - 1:].contiguous()
+        # the step as one call (append inside the decode kernels) ...
         cache = pdec.KVCache(H, L, D, q.dtype, s, q.device)
         cache.append(k[:, :L - 1], v[:, :L - 1])
-        kn, vn = k[:, L - 1:].contiguous(), v[:, L - 1:].contiguous()
-        cache.append(kn, vn)
-        launch = cache.prepare(q[:, L - 1:].contiguous(), wl.union)
+        fused = cache.prepare(qn, wl.union, k_new=kn, v_new=vn)
+        # ... and as pa_kv_append followed by the decode call, on a second cache
+        cache2 = pdec.KVCache(H, L, D, q.dtype, s, q.device)
+        cache2.append(k[:, :L - 1], v[:, :L - 1])
+        cache2.append(kn, vn)
+        attend = cache2.prepare(qn, wl.union)
         lib = _lib.lib()
-        app_args = (_lib.ptr(kn), _lib.ptr(vn), kn.stride(0), kn.stride(1), _lib.ptr(cache.k), _lib.ptr(cache.v),
-                    cache.k.stride(0), cache.k.stride(1), H, 1, D, _lib.dtype_code(kn), L, L - 1, cache.residue)
+        app_args = (_lib.ptr(kn), _lib.ptr(vn), kn.stride(0), kn.stride(1), _lib.ptr(cache2.k), _lib.ptr(cache2.v),
+                    cache2.k.stride(0), cache2.k.stride(1), H, 1, D, _lib.dtype_code(kn), L, L - 1, cache2.residue)
 
-        def step():
+        def separate():
             _lib.check(lib.pa_kv_append(*app_args, _lib.stream_of(kn)), "pa_kv_append")
-            launch()
+            attend()
 
-        step()
-        torch.cuda.synchronize()
-        eager_out = launch.out.clone()
-        g = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(g, stream=side):
-                step()
-        torch.cuda.current_stream().wait_stream(side)
-        for _ in range(warmup):
-            g.replay()
-        torch.cuda.synchronize()
-        same = torch.equal(launch.out, eager_out)
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        ev[0].record()
-        for _ in range(reps):
-            g.replay()
-        ev[1].record()
-        torch.cuda.synchronize()
-        ms = ev[0].elapsed_time(ev[1]) / reps
-        # eager steps for comparison (host launch overhead included)
-        t0 = time.perf_counter()
-        for _ in range(50):
+        def timed(step, out_t):
             step()
-        torch.cuda.synchronize()
-        eager_ms = (time.perf_counter() - t0) * 1e3 / 50
+            torch.cuda.synchronize()
+            eager_out = out_t.clone()
+            g = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(g, stream=side):
+                    step()
+            torch.cuda.current_stream().wait_stream(side)
+            for _ in range(warmup):
+                g.replay()
+            torch.cuda.synchronize()
+            same = torch.equal(out_t, eager_out)
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record()
+            for _ in range(reps):
+                g.replay()
+            ev[1].record()
+            torch.cuda.synchronize()
+            ms = ev[0].elapsed_time(ev[1]) / reps
+            # eager steps for comparison (host launch overhead included)
+            t0 = time.perf_counter()
+            for _ in range(50):
+                step()
+            torch.cuda.synchronize()
+            return ms, (time.perf_counter() - t0) * 1e3 / 50, same
+
+        ms, eager_ms, same = timed(fused, fused.out)
+        sep_ms, sep_eager_ms, _ = timed(separate, attend.out)
+        agree = torch.equal(fused.out, attend.out)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out["identity" if s <= 1 else f"rp{s}"] = dict(
             ms_per_token=round(ms, 5), eager_ms_per_token=round(eager_ms, 5), tokens_per_s=round(1e3 / ms, 1),
-            graph_equals_eager=same, bytes=nbytes, gb_per_s=round(gbs, 1),
+            separate_ms_per_token=round(sep_ms, 5), separate_eager_ms_per_token=round(sep_eager_ms, 5),
+            graph_equals_eager=same, one_call_equals_separate=agree, bytes=nbytes, gb_per_s=round(gbs, 1),
             roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_GBPS, unit="GB/s",
                           frac=round(gbs / HBM_GBPS, 5)))
-        del cache, launch, g
-    return dict(live_keys=live, heads=H, context=L, note="one decode step (append + attend), batch 1, "
+        del cache, cache2, fused, attend
+    return dict(live_keys=live, heads=H, context=L, note="one decode step (append + attend in one call), batch 1, "
                 "HIP graph replay; algorithmic bytes = live K/V rows + appended rows + q + o", **out)
 
 
@@ -541,8 +553,9 @@ def log_result(r):
             f"on {ib['cpu_threads']} threads ({ib['speedup']:.0f}x)")
     if r.get("decode"):
         dd = r["decode"]
-        log("[bench]   decode (append + attend, 1 token): " + ", ".join(
-            f"{b} {dd[b]['ms_per_token'] * 1e3:.1f} us ({dd[b]['gb_per_s']:.0f} GB/s)"
+        log("[bench]   decode (append + attend in one call, 1 token): " + ", ".join(
+            f"{b} {dd[b]['ms_per_token'] * 1e3:.1f} us ({dd[b]['gb_per_s']:.0f} GB/s; as two calls "
+            f"{dd[b]['separate_ms_per_token'] * 1e3:.1f} us)"
             for b in dd if isinstance(dd[b], dict)))
     if r.get("backward"):
         bw = r["backward"]

@@ -330,7 +330,15 @@ int pa_kv_append(const void* k_new, const void* v_new, int64_t new_sb, int64_t n
  * q, o [BH, nq, D], lse [BH, nq] fp32 or NULL; scale <= 0 means 1/sqrt(D).  The split
  * partials go to `workspace`, whose size pa_decode_workspace returns for these
  * arguments (it depends on BH, nq, D, capacity, length and residue_s).  A PA_DENSE
- * mask must hold rows up to qpos0 + nq - 1. */
+ * mask must hold rows up to qpos0 + nq - 1.
+ *
+ * With n_new > 0 the call also appends: rows j = 0..n_new-1 of k_new / v_new [BH, n_new,
+ * D] (strides new_sb / new_sn in elements, 16-byte aligned rows) are the tokens at
+ * original positions new_pos0 + j, as pa_kv_append would write them, and the attention
+ * reads them from k_new / v_new (the split's work-group that owns a new row also writes
+ * it to the cache), so one call does what pa_kv_append followed by pa_decode_fwd does.
+ * n_new <= 8, new_pos0 >= 0 and new_pos0 + n_new <= length.  n_new = 0 (the zero-filled
+ * default) appends nothing. */
 typedef struct pa_decode_args {
   const void* q;
   int64_t q_sb, q_sn;
@@ -351,6 +359,10 @@ typedef struct pa_decode_args {
   int64_t lse_sb;
   void* workspace;
   int64_t workspace_bytes;
+  const void* k_new;
+  const void* v_new;
+  int64_t new_sb, new_sn;
+  int64_t n_new, new_pos0;
 } pa_decode_args;
 
 int pa_decode_workspace(const pa_decode_args* args, int64_t* bytes);

@@ -59,7 +59,8 @@ class PaDecodeArgs(ctypes.Structure):
                 ("capacity", c_i64), ("length", c_i64), ("residue_s", c_i32), ("mask", PaMask),
                 ("BH", c_i64), ("D", c_i32), ("dtype", c_i32), ("scale", c_f32),
                 ("o", c_vp), ("o_sb", c_i64), ("o_sn", c_i64), ("lse", c_vp), ("lse_sb", c_i64),
-                ("workspace", c_vp), ("workspace_bytes", c_i64)]
+                ("workspace", c_vp), ("workspace_bytes", c_i64), ("k_new", c_vp), ("v_new", c_vp),
+                ("new_sb", c_i64), ("new_sn", c_i64), ("n_new", c_i64), ("new_pos0", c_i64)]
 
 
 class PaAttnBwdArgs(ctypes.Structure):

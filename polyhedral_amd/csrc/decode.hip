@@ -44,6 +44,12 @@ struct DecK {
   Pred pred;
   float* o_part;    // [BH][n_split][nq][D]
   float* lse_part;  // [BH][n_split][nq]
+  // tokens appended by this call (n_new = 0: none): their K / V rows are read from
+  // k_new / v_new, and the work-group owning a new row writes it to the cache
+  const char* k_new;
+  const char* v_new;
+  int64_t new_sb, new_sn;  // bytes
+  int64_t n_new, new_pos0;
 };
 
 // 16 bytes of a K row against 16 bytes of a query row, accumulated in fp32; one or two
@@ -155,6 +161,24 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
   const char* kseg = a.k + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
   const char* vseg = a.v + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
   const int64_t rowb = a.c_sn * ESZ;
+  const char* knew = a.k_new + bh * a.new_sb;
+  const char* vnew = a.v_new + bh * a.new_sb;
+
+  // The appended rows this work-group owns (entry e of this class's segment in one of its
+  // groups) go to the cache: thread u copies 16-byte unit u % NC of the K (u < NC) or V
+  // row.  Nothing in this launch reads them back from the cache: the keys' lanes below
+  // take them from k_new / v_new.
+  for (int64_t j = 0; j < a.n_new; ++j) {
+    const int64_t t = a.new_pos0 + j;
+    const int64_t e = t / a.s;
+    if (t - e * a.s != cls || (e >> 8) % a.per_class != jc) continue;
+    if (tid < 2 * NC) {
+      const int uu = tid % NC;
+      const char* src = (tid < NC ? knew : vnew) + j * a.new_sn + 16 * uu;
+      char* dst = const_cast<char*>(tid < NC ? kseg : vseg) + e * rowb + 16 * uu;
+      *reinterpret_cast<du4*>(dst) = *reinterpret_cast<const du4*>(src);
+    }
+  }
 
   float m[MQ], lsum[MQ], o[MQ][DPL];
 #pragma unroll
@@ -176,6 +200,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
     }
     const uint64_t any = __ballot(lv != 0u);
     if (any == 0ull) continue;
+    // keys appended by this call: read from k_new / v_new
+    const int64_t jn = (int64_t)t - a.new_pos0;
+    const bool isnew = idx < i1 && jn >= 0 && jn < a.n_new;
+    const uint64_t newm = a.n_new ? __ballot(isnew) : 0ull;
 
     // the V rows of the keys live for some query, into this wave's buffer (lanes of a dead
     // row are masked off; a DMA instruction whose rows are all dead is skipped), and the
@@ -186,15 +214,27 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
     for (int r = 0; r < 64 / RPI; ++r) {
       if ((any >> (r * RPI)) & ((1ull << RPI) - 1ull)) {
         const int row = r * RPI + lane / LPR;
-        if ((any >> row) & 1ull)
+        if (((any & ~newm) >> row) & 1ull)
           lds_dma16(vbw + r * 1024, vblk, (uint32_t)(row * rowb + 16 * (lane % LPR)));
+      }
+    }
+    if (newm & any) {
+      // an appended row's 16-byte units, from v_new into the same place of the buffer
+#pragma unroll
+      for (int r = 0; r < 64 / RPI; ++r) {
+        const int row = r * RPI + lane / LPR;
+        if (((newm & any) >> row) & 1ull) {
+          const int64_t jr = ((b0 + row) * a.s + cls) - a.new_pos0;
+          *reinterpret_cast<du4*>(vbuf + w * 64 * RB + r * 1024 + 16 * lane) =
+              *reinterpret_cast<const du4*>(vnew + jr * a.new_sn + 16 * (lane % LPR));
+        }
       }
     }
     du4 kr[NC];
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) kr[cc] = du4{0u, 0u, 0u, 0u};
     if (lv) {
-      const char* kp = kseg + idx * rowb;
+      const char* kp = isnew ? knew + jn * a.new_sn : kseg + idx * rowb;
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) kr[cc] = *reinterpret_cast<const du4*>(kp + 16 * cc);
     }
@@ -434,6 +474,17 @@ int check_decode(const pa_decode_args* x) {
   PA_CHECK_ARG(al(x->q, x->q_sb, x->q_sn) && al(x->k_cache, x->c_sb, x->c_sn) && al(x->v_cache, x->c_sb, x->c_sn),
                "pa_decode: q and cache rows must be 16-byte aligned");
   PA_CHECK_ARG(x->c_sn >= x->D && x->q_sn >= x->D, "pa_decode: row strides below D");
+  PA_CHECK_ARG(x->n_new >= 0 && x->n_new <= kDecMaxQ, "pa_decode: n_new=%lld not in 0..%d", (long long)x->n_new,
+               kDecMaxQ);
+  if (x->n_new > 0) {
+    PA_CHECK_ARG(x->k_new && x->v_new, "pa_decode: null k_new / v_new");
+    PA_CHECK_ARG(al(x->k_new, x->new_sb, x->new_sn) && al(x->v_new, x->new_sb, x->new_sn),
+                 "pa_decode: k_new / v_new rows must be 16-byte aligned");
+    PA_CHECK_ARG(x->new_sn >= x->D, "pa_decode: new_sn below D");
+    PA_CHECK_ARG(x->new_pos0 >= 0 && x->new_pos0 + x->n_new <= x->length,
+                 "pa_decode: appended positions %lld..%lld outside the attended length %lld",
+                 (long long)x->new_pos0, (long long)(x->new_pos0 + x->n_new), (long long)x->length);
+  }
   return PA_OK;
 }
 
@@ -553,6 +604,13 @@ int decode_launch(const pa_decode_args* x, const Plan& p, float* ws, hipStream_t
   k.pred = pa::make_pred(x->mask);
   k.o_part = ws;
   k.lse_part = ws ? ws + x->BH * (int64_t)p.n_split * x->nq * x->D : nullptr;
+  const int64_t esz = x->dtype == PA_F32 ? 4 : 2;
+  k.n_new = x->n_new;
+  k.new_pos0 = x->new_pos0;
+  k.k_new = x->n_new ? static_cast<const char*>(x->k_new) : nullptr;
+  k.v_new = x->n_new ? static_cast<const char*>(x->v_new) : nullptr;
+  k.new_sb = x->n_new ? x->new_sb * esz : 0;
+  k.new_sn = x->n_new ? x->new_sn * esz : 0;
   if (p.n_split > 0) {
     int r = PA_OK;
     if (x->dtype == PA_BF16)

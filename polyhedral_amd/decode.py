@@ -73,9 +73,7 @@ class KVCache:
         """Cache rows of original positions t."""
         return basis_rows(t, self.residue, self.capacity)
 
-    def append(self, k_new, v_new):
-        """Append the tokens at original positions length .. length + n - 1
-        (k_new, v_new: [BH, n, D] in the cache's dtype); one launch writes them all."""
+    def _check_new(self, k_new, v_new):
         _lib.require_device(k_new, v_new)
         for t, name in ((k_new, "k_new"), (v_new, "v_new")):
             _rows_ok(t, name)
@@ -87,6 +85,12 @@ class KVCache:
         n = k_new.shape[1]
         if self.length + n > self.capacity:
             raise ValueError(f"appending {n} tokens to {self.length} exceeds the capacity {self.capacity}")
+        return n
+
+    def append(self, k_new, v_new):
+        """Append the tokens at original positions length .. length + n - 1
+        (k_new, v_new: [BH, n, D] in the cache's dtype); one launch writes them all."""
+        n = self._check_new(k_new, v_new)
         with torch.cuda.device(self.device):
             _lib.check(_lib.lib().pa_kv_append(
                 _lib.ptr(k_new), _lib.ptr(v_new), k_new.stride(0), k_new.stride(1), _lib.ptr(self.k),
@@ -94,25 +98,40 @@ class KVCache:
                 self.capacity, self.length, self.residue, _lib.stream_of(self.k)), "pa_kv_append")
         self.length += n
 
-    def prepare(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None, static_scratch=False):
+    def prepare(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None, static_scratch=False,
+                k_new=None, v_new=None):
         """A DecodeLaunch of q [BH, nq, D] (nq <= 8, queries at original positions qpos0 ..
         qpos0 + nq - 1, by default the last nq tokens) against the first ``length`` cached
         tokens (default: all).  mask: a polyattn mask object, a MaskSpec or a DeviceMask
         without permutation tables; the cache's basis is applied by the kernel.
         static_scratch: launch pa_decode_fwd_static, which allocates nothing (its split
         partials go to the library's 8 MiB per-GPU scratch; launches that overlap on one
-        GPU race)."""
+        GPU race).
+        k_new, v_new [BH, n, D] (n <= 8): the launch also appends these tokens at positions
+        length .. length + n - 1, in the same kernels as the attention (one launch less
+        than append() then attend); the cache's length counts them from this call on,
+        and every run of the launch writes them again."""
         _lib.require_device(q)
+        n_new = 0
+        if k_new is not None or v_new is not None:
+            if k_new is None or v_new is None:
+                raise ValueError("k_new and v_new go together")
+            n_new = self._check_new(k_new, v_new)
+            if n_new > MAX_QUERIES:
+                raise ValueError(f"{n_new} new tokens: one call appends at most {MAX_QUERIES}")
         _rows_ok(q, "q")
         BH, nq, D = q.shape
         if BH != self.BH or D != self.D or q.dtype != self.k.dtype:
             raise ValueError(f"q must be [{self.BH}, nq, {self.D}] {self.k.dtype}")
         if not 1 <= nq <= MAX_QUERIES:
             raise ValueError(f"nq={nq}: decoding takes 1..{MAX_QUERIES} query rows per call")
-        L = self.length if length is None else int(length)
-        if not 0 <= L <= self.length:
-            raise ValueError(f"length={L} outside 0..{self.length}")
-        qpos0 = self.length - nq if qpos0 is None else int(qpos0)
+        new_pos0 = self.length
+        total = self.length + n_new
+        L = total if length is None else int(length)
+        lo = new_pos0 + n_new if n_new else 0   # the appended tokens are attended
+        if not lo <= L <= total:
+            raise ValueError(f"length={L} outside {lo}..{total}")
+        qpos0 = total - nq if qpos0 is None else int(qpos0)
         if qpos0 < 0:
             raise ValueError(f"query positions start at {qpos0} < 0")
         dev = self.device
@@ -132,21 +151,30 @@ class KVCache:
         a.BH, a.D, a.dtype = BH, D, _lib.dtype_code(q)
         a.scale = float(scale) if scale else float(D ** -0.5)
         a.o, a.o_sb, a.o_sn = _lib.ptr(o), o.stride(0), o.stride(1)
+        keep_new = []
+        if n_new:
+            a.k_new, a.v_new, a.new_sb, a.new_sn = _lib.ptr(k_new), _lib.ptr(v_new), k_new.stride(0), k_new.stride(1)
+            a.n_new, a.new_pos0 = n_new, new_pos0
+            keep_new = [k_new, v_new]
         if lse is not None:
             _lib.require_device(lse)
             if lse.dtype != torch.float32 or lse.shape != (BH, nq) or lse.stride(1) != 1:
                 raise ValueError("lse must be float32 [BH, nq] with unit stride")
             a.lse, a.lse_sb = _lib.ptr(lse), lse.stride(0)
         if static_scratch:
-            return DecodeLaunch(a, [q, o, lse, dm, self.k, self.v], o, dev, static_scratch=True)
-        nbytes = ctypes.c_int64(0)
-        _lib.check(_lib.lib().pa_decode_workspace(ctypes.byref(a), ctypes.byref(nbytes)), "pa_decode_workspace")
-        ws = torch.empty(max(1, (nbytes.value + 3) // 4), dtype=torch.float32, device=dev)
-        a.workspace, a.workspace_bytes = _lib.ptr(ws), ws.numel() * 4
-        return DecodeLaunch(a, [q, o, lse, dm, ws, self.k, self.v], o, dev)
+            launch = DecodeLaunch(a, [q, o, lse, dm, self.k, self.v] + keep_new, o, dev, static_scratch=True)
+        else:
+            nbytes = ctypes.c_int64(0)
+            _lib.check(_lib.lib().pa_decode_workspace(ctypes.byref(a), ctypes.byref(nbytes)), "pa_decode_workspace")
+            ws = torch.empty(max(1, (nbytes.value + 3) // 4), dtype=torch.float32, device=dev)
+            a.workspace, a.workspace_bytes = _lib.ptr(ws), ws.numel() * 4
+            launch = DecodeLaunch(a, [q, o, lse, dm, ws, self.k, self.v] + keep_new, o, dev)
+        self.length = total
+        return launch
 
-    def attend(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None, static_scratch=False):
+    def attend(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None, static_scratch=False,
+               k_new=None, v_new=None):
         """o [BH, nq, D]: see prepare."""
-        launch = self.prepare(q, mask, scale, qpos0, out, lse, length, static_scratch)
+        launch = self.prepare(q, mask, scale, qpos0, out, lse, length, static_scratch, k_new, v_new)
         with torch.cuda.device(self.device):
             return launch()

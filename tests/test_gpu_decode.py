@@ -124,6 +124,58 @@ def test_bases_agree_at_the_headline_size(gpu):
     assert (outs[0] - outs[1]).abs().max().item() < 2e-2
 
 
+@pytest.mark.parametrize("static", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("residue", [0, 16])
+@pytest.mark.parametrize("n_new,nq", [(1, 1), (3, 3), (8, 8), (2, 5)])
+def test_append_in_the_decode_call_equals_append_then_attend(gpu, residue, dtype, n_new, nq, static):
+    """prepare(..., k_new, v_new) appends in the decode kernels: the same output, log-sum-exp
+    and cache as pa_kv_append followed by the decode call, bit for bit.  The new rows are
+    not in the cache before the call, so reading them from there would show."""
+    BH, cap, L0, name = 3, 2048, 1500, "band256+lat16"
+    D = 64 if dtype == torch.float32 else 128
+    q, k, v = make_qkv(BH, cap, D, dtype, seed=11 + n_new)
+    caches = [pdec.KVCache(BH, cap, D, dtype, residue, gpu) for _ in range(2)]
+    for c in caches:
+        _fill(c, k, v, [L0], gpu)
+    kn, vn = k[:, L0:L0 + n_new].to(gpu), v[:, L0:L0 + n_new].to(gpu)
+    qq = q[:, L0 + n_new - nq:L0 + n_new].to(gpu)
+    lse = [torch.empty(BH, nq, device=gpu) for _ in range(2)]
+    caches[0].append(kn, vn)
+    o0 = caches[0].attend(qq, numpy_mask(name), lse=lse[0], static_scratch=static)
+    o1 = caches[1].attend(qq, numpy_mask(name), lse=lse[1], static_scratch=static, k_new=kn, v_new=vn)
+    torch.cuda.synchronize()
+    assert caches[0].length == caches[1].length == L0 + n_new
+    assert torch.equal(o0, o1) and torch.equal(lse[0], lse[1])
+    assert torch.equal(caches[0].k, caches[1].k) and torch.equal(caches[0].v, caches[1].v)
+    qpos0 = L0 + n_new - nq
+    want, _ = oatt.dense_attention(as64(q[:, qpos0:L0 + n_new]), as64(k[:, :L0 + n_new]), as64(v[:, :L0 + n_new]),
+                                   lambda r0, r1: om.rows(om.NAMED[name], qpos0 + r0, qpos0 + r1, L0 + n_new))
+    check_close(o1, want, dtype, f"decode with append s={residue} n_new={n_new} nq={nq}")
+
+
+def test_append_in_the_decode_call_at_the_headline_size(gpu):
+    """band-256 | lattice-16, L = 16384, 32 heads: the newest token appended and decoded in
+    one call, replayed (each run rewrites the same rows), against append then decode."""
+    H, L, D, name = 32, 16384, 128, "band256+lat16"
+    q, k, v = make_qkv(H, L, D, torch.bfloat16, seed=0)
+    for s in (0, 16):
+        a = pdec.KVCache(H, L, D, torch.bfloat16, s, gpu)
+        b = pdec.KVCache(H, L, D, torch.bfloat16, s, gpu)
+        for c in (a, b):
+            _fill(c, k, v, [L - 1], gpu)
+        kn, vn, qn = (x[:, L - 1:].contiguous().to(gpu) for x in (k, v, q))
+        a.append(kn, vn)
+        want = a.attend(qn, numpy_mask(name))
+        launch = b.prepare(qn, numpy_mask(name), k_new=kn, v_new=vn)
+        for _ in range(3):
+            got = launch()
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"s={s}"
+        assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+        del a, b, launch
+
+
 def test_decode_argument_errors(gpu):
     BH, cap, D = 1, 256, 128
     cache = pdec.KVCache(BH, cap, D, torch.bfloat16, 16, gpu)
