@@ -344,8 +344,8 @@ typedef struct pa_decode_args {
   int64_t q_sb, q_sn;
   int32_t nq;
   int64_t qpos0;
-  const void* k_cache;
-  const void* v_cache;
+  void* k_cache;  /* read; written only for the rows appended by the call (n_new > 0) */
+  void* v_cache;
   int64_t c_sb, c_sn;
   int64_t capacity, length;
   int32_t residue_s;

@@ -35,8 +35,8 @@ typedef uint32_t du4 __attribute__((ext_vector_type(4)));
 struct DecK {
   const char* q;
   int64_t q_sb, q_sn;  // elements
-  const char* k;
-  const char* v;
+  char* k;  // the cache (written only for the rows this call appends)
+  char* v;
   int64_t c_sb, c_sn;  // elements
   int64_t qpos0, length, Q, chunk;
   int32_t nq, s, per_class, n_split;
@@ -161,8 +161,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
   const char* kseg = a.k + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
   const char* vseg = a.v + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
   const int64_t rowb = a.c_sn * ESZ;
-  const char* knew = a.k_new + bh * a.new_sb;
-  const char* vnew = a.v_new + bh * a.new_sb;
+  const char* knew = a.n_new ? a.k_new + bh * a.new_sb : nullptr;
+  const char* vnew = a.n_new ? a.v_new + bh * a.new_sb : nullptr;
 
   // The appended rows this work-group owns (entry e of this class's segment in one of its
   // groups) go to the cache: thread u copies 16-byte unit u % NC of the K (u < NC) or V
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
     if (tid < 2 * NC) {
       const int uu = tid % NC;
       const char* src = (tid < NC ? knew : vnew) + j * a.new_sn + 16 * uu;
-      char* dst = const_cast<char*>(tid < NC ? kseg : vseg) + e * rowb + 16 * uu;
+      char* dst = (tid < NC ? a.k : a.v) + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ + e * rowb + 16 * uu;
       *reinterpret_cast<du4*>(dst) = *reinterpret_cast<const du4*>(src);
     }
   }
@@ -588,8 +588,8 @@ int decode_launch(const pa_decode_args* x, const Plan& p, float* ws, hipStream_t
   k.q = static_cast<const char*>(x->q);
   k.q_sb = x->q_sb;
   k.q_sn = x->q_sn;
-  k.k = static_cast<const char*>(x->k_cache);
-  k.v = static_cast<const char*>(x->v_cache);
+  k.k = static_cast<char*>(x->k_cache);
+  k.v = static_cast<char*>(x->v_cache);
   k.c_sb = x->c_sb;
   k.c_sn = x->c_sn;
   k.qpos0 = x->qpos0;
