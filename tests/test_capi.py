@@ -203,6 +203,35 @@ def test_decode_rejects_more_residue_classes_than_the_merge_takes():
         pdec.KVCache(1, 16384, 128, residue=8192, device="cpu")
 
 
+def test_decode_append_arguments_are_checked():
+    """The tokens a decode call appends (n_new > 0) must be at most 8, inside the attended
+    length, with both row pointers given and 16-byte aligned; the host checks refuse
+    them before touching a device."""
+    lib = _lib.lib()
+    a = _lib.PaDecodeArgs()
+    buf = (ctypes.c_int64 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    a.q, a.k_cache, a.v_cache, a.o = p, p, p, p
+    a.nq, a.BH, a.D, a.dtype = 1, 2, 128, _lib.PA_BF16
+    a.q_sb, a.q_sn, a.c_sb, a.c_sn, a.o_sb, a.o_sn = 128, 128, 1024 * 128, 128, 128, 128
+    a.capacity, a.length, a.residue_s = 1024, 100, 16
+    a.mask.n_include = 1
+    n = ctypes.c_int64(0)
+    assert lib.pa_decode_workspace(ctypes.byref(a), ctypes.byref(n)) == _lib.PA_OK
+    a.n_new, a.new_pos0, a.new_sb, a.new_sn = 1, 99, 128, 128
+    assert lib.pa_decode_workspace(ctypes.byref(a), ctypes.byref(n)) == _lib.PA_E_INVALID
+    assert b"k_new" in lib.pa_last_error()
+    a.k_new, a.v_new = p, p
+    assert lib.pa_decode_workspace(ctypes.byref(a), ctypes.byref(n)) == _lib.PA_OK
+    for field, value, text in (("n_new", 9, b"n_new=9"), ("new_pos0", 100, b"outside the attended length"),
+                               ("new_sn", 100, b"16-byte aligned")):
+        old = getattr(a, field)
+        setattr(a, field, value)
+        assert lib.pa_decode_workspace(ctypes.byref(a), ctypes.byref(n)) == _lib.PA_E_INVALID, field
+        assert text in lib.pa_last_error(), (field, lib.pa_last_error())
+        setattr(a, field, old)
+
+
 def test_static_decode_rejects_a_workspace_and_partials_beyond_its_scratch():
     """pa_decode_fwd_static takes no workspace, and refuses (before touching a device) a
     call whose split partials exceed its 8 MiB scratch."""
