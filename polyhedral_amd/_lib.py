@@ -14,7 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libpolyattn_amd.s
 PA_OK, PA_E_INVALID, PA_E_HIP, PA_E_UNSUPPORTED = 0, -1, -2, -3
 PA_F32, PA_F16, PA_BF16 = 0, 1, 2
 MAX_TERMS = 8
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 c_i32, c_i64, c_f32, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 

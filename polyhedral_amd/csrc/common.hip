@@ -72,4 +72,4 @@ int check_mask(const pa_mask* m, int64_t N) {
 
 extern "C" const char* pa_last_error(void) { return pa::g_err; }
 
-extern "C" int32_t pa_abi_version(void) { return 18; }
+extern "C" int32_t pa_abi_version(void) { return 19; }
