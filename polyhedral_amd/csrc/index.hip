@@ -2,10 +2,11 @@
 // KV tiles.  Replaces gpu/blockindex.py:32-51 (build), which materialises the N x N
 // mask on the host and tiles it with numpy any/all.
 //
-// Phase 1 (classify): one work-group per query block walks every KV column in
-// chunks of 256, evaluates the predicate for the block's BQ rows and folds the
-// result into per-tile codes: 2 bits (some live / all live) per wave group of
-// 32 query rows x min(A, 32) columns.  Wave ballots do the column reduction.
+// Phase 1 (classify): work-groups (query block, column split) walk the KV columns in
+// chunks of 256 (split j takes chunks j, j + splits, ...), evaluate the predicate for
+// the block's BQ rows and fold the result into per-tile codes: 2 bits (some live / all
+// live) per wave group of 32 query rows x min(A, 32) columns.  Wave ballots do the
+// column reduction; a query block's list length is summed over its splits.
 // Phase 2 (compact): one work-group per query block scans the tile codes and
 // writes the ascending, zero-padded kv_idx / kv_partial / kv_wave_bits rows.
 #include "common.hpp"
@@ -16,8 +17,18 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kChunk = 256;  // columns per pass, one per thread
 
-__global__ void zero_totals_kernel(unsigned long long* totals) {
-  if (threadIdx.x < 3) totals[threadIdx.x] = 0ull;
+__global__ void zero_totals_kernel(unsigned long long* totals, int32_t* kv_num, int32_t nq) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 3) totals[i] = 0ull;
+  if (i < nq) kv_num[i] = 0;
+}
+
+// The longest list, once every split has added its count.
+__global__ void max_list_kernel(const int32_t* kv_num, int32_t nq, unsigned long long* totals) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  int32_t v = i < nq ? kv_num[i] : 0;
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_down(v, off, 64));
+  if ((threadIdx.x & 63) == 0 && v > 0) atomicMax(&totals[2], (unsigned long long)v);
 }
 
 __global__ __launch_bounds__(kThreads) void classify_kernel(const Pred pred, int32_t N, int32_t BQ,
@@ -33,6 +44,7 @@ __global__ __launch_bounds__(kThreads) void classify_kernel(const Pred pred, int
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int qb = blockIdx.x;
+  const int split = blockIdx.y, splits = gridDim.y;
   const int nk = N / A;
   const int rg_rows = BQ < 32 ? BQ : 32;   // rows per wave group
   const int n_rg = BQ / rg_rows;
@@ -49,7 +61,7 @@ __global__ __launch_bounds__(kThreads) void classify_kernel(const Pred pred, int
   int32_t live_count = 0;
   int32_t tiles_listed = 0;  // meaningful in thread 0 only
 
-  for (int c0 = 0; c0 < N; c0 += kChunk) {
+  for (int c0 = split * kChunk; c0 < N; c0 += splits * kChunk) {
     if (tid < kChunk / 16) tile_code[tid] = 0u;
     __syncthreads();
 
@@ -110,10 +122,11 @@ __global__ __launch_bounds__(kThreads) void classify_kernel(const Pred pred, int
     long long tot = 0;
     for (int i = 0; i < kThreads / 64; ++i) tot += red_live[i];
     tiles_listed = red_tiles;
-    kv_num[qb] = tiles_listed;
-    atomicAdd(&totals[0], (unsigned long long)tiles_listed);
-    atomicAdd(&totals[1], (unsigned long long)tot);
-    atomicMax(&totals[2], (unsigned long long)tiles_listed);
+    if (tiles_listed) {
+      atomicAdd(&kv_num[qb], tiles_listed);
+      atomicAdd(&totals[0], (unsigned long long)tiles_listed);
+    }
+    if (tot) atomicAdd(&totals[1], (unsigned long long)tot);
   }
 }
 
@@ -181,11 +194,21 @@ extern "C" int pa_index_classify(const pa_mask* mask, int64_t N, int32_t BQ, int
   if (int rc = pa::check_mask(mask, N)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const pa::Pred pred = pa::make_pred(*mask);
-  hipLaunchKernelGGL(pa::zero_totals_kernel, dim3(1), dim3(64), 0, s, totals);
+  const int64_t nq = N / BQ;
+  hipLaunchKernelGGL(pa::zero_totals_kernel, dim3((unsigned)((nq + 3 + 255) / 256)), dim3(256), 0, s, totals, kv_num,
+                     (int32_t)nq);
   PA_LAUNCH_CHECK("zero_totals_kernel");
-  hipLaunchKernelGGL(pa::classify_kernel, dim3((unsigned)(N / BQ)), dim3(pa::kThreads), 0, s, pred,
+  // enough column splits for about 2048 work-groups (the chip holds ~2048 of 256 threads)
+  const int64_t chunks = (N + pa::kChunk - 1) / pa::kChunk;
+  int64_t splits = (2048 + nq - 1) / nq;
+  if (splits > chunks) splits = chunks;
+  if (splits < 1) splits = 1;
+  hipLaunchKernelGGL(pa::classify_kernel, dim3((unsigned)nq, (unsigned)splits), dim3(pa::kThreads), 0, s, pred,
                      (int32_t)N, BQ, A, tile_codes, kv_num, totals);
   PA_LAUNCH_CHECK("classify_kernel");
+  hipLaunchKernelGGL(pa::max_list_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, kv_num,
+                     (int32_t)nq, totals);
+  PA_LAUNCH_CHECK("max_list_kernel");
   return PA_OK;
 }
 
