@@ -143,7 +143,8 @@ def measure_decode(wl, q, k, v, residues=(0, 16), reps=200, warmup=20):
     token's K / V appended and its query row attended to the cache, in one pa_decode_fwd
     call (split kernel + merge; the split's work-group owning the new row writes it,
     rewriting the same row every step), captured in a HIP graph and replayed (the step is
-    a few microseconds of kernels).  The same step as pa_kv_append then pa_decode_fwd is
+    a few microseconds of kernels; ~150 ms of replays settle the clocks, then the median
+    of 3 rounds).  The same step as pa_kv_append then pa_decode_fwd is
     timed beside it (`separate_ms_per_token`), and both are also timed launched eagerly.
     Algorithmic bytes: the live keys' K and V rows, the appended rows, q and o."""
     import ctypes
@@ -187,17 +188,24 @@ def measure_decode(wl, q, k, v, residues=(0, 16), reps=200, warmup=20):
                 with torch.cuda.graph(g, stream=side):
                     step()
             torch.cuda.current_stream().wait_stream(side)
-            for _ in range(warmup):
-                g.replay()
-            torch.cuda.synchronize()
+            # clocks settle under ~150 ms of replays (a step is tens of microseconds, and the
+            # GPU may have idled since the forward's timing), then 3 rounds, the median
+            t_end = time.perf_counter() + 0.15
+            while time.perf_counter() < t_end:
+                for _ in range(warmup):
+                    g.replay()
+                torch.cuda.synchronize()
             same = torch.equal(out_t, eager_out)
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-            ev[0].record()
-            for _ in range(reps):
-                g.replay()
-            ev[1].record()
-            torch.cuda.synchronize()
-            ms = ev[0].elapsed_time(ev[1]) / reps
+            rounds = []
+            for _ in range(3):
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                ev[0].record()
+                for _ in range(reps):
+                    g.replay()
+                ev[1].record()
+                torch.cuda.synchronize()
+                rounds.append(ev[0].elapsed_time(ev[1]) / reps)
+            ms = sorted(rounds)[1]
             # eager steps for comparison (host launch overhead included)
             t0 = time.perf_counter()
             for _ in range(50):
