@@ -209,18 +209,23 @@ typedef const __attribute__((address_space(3))) uint32_t lds_u32;
 // LDS DMA (global_load_lds_dwordx4 / _dword): lane l writes LDS[m0 + 16 l] / LDS[m0 + 4 l]
 // from gbase + voff.  Issued from inline assembly, so the compiler, which cannot tell
 // which LDS bytes a DMA writes, does not wait for it before unrelated LDS reads; the
-// caller waits itself (dma_wait_all, then a work-group barrier).
+// caller waits itself (dma_wait_all, then a work-group barrier).  An LDS DMA that reads
+// M0 right after a scalar write of M0 needs one wait state, which the compiler's hazard
+// pass does not insert inside inline assembly: hence the s_nop 0.
 __device__ __forceinline__ void dma_x4(uint32_t m0, const char* gbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(gbase)
+               : "m0");
 }
 __device__ __forceinline__ void dma_x1(uint32_t m0, const char* gbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(voff), "s"(gbase)
+               : "m0");
 }
 __device__ __forceinline__ void dma_wait_all() { asm volatile("s_waitcnt vmcnt(0)"); }
 // The same DMA with agent-scope coherence (sc1): reads data another work-group published
 // with agent-scope stores, whichever XCD's L2 it went through.
 __device__ __forceinline__ void dma_x4_sc1(uint32_t m0, const char* gbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 sc1" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 sc1" ::"s"(m0), "v"(voff),
+               "s"(gbase) : "m0");
 }
 // A 16-byte agent-scope store (sc1: written through to memory, visible to every XCD once
 // complete); the caller waits for it (s_waitcnt vmcnt) before publishing.  On gfx950 a VALU

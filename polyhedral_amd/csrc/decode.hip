@@ -99,9 +99,11 @@ struct Dec<float> {
   __device__ static float hi(uint32_t w) { return __builtin_bit_cast(float, w); }
 };
 
-// LDS DMA of 16 bytes per lane: lane l writes LDS[m0 + 16 l] from gbase + voff.
+// LDS DMA of 16 bytes per lane: lane l writes LDS[m0 + 16 l] from gbase + voff (one wait
+// state between the scalar write of M0 and the DMA that reads it).
 __device__ __forceinline__ void lds_dma16(uint32_t m0, const char* gbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(gbase) : "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(gbase)
+               : "m0");
 }
 
 __device__ __forceinline__ float wave_max(float x) {
