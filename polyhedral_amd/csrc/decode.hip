@@ -19,6 +19,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <numeric>
 
 #include "common.hpp"
 
@@ -28,7 +29,8 @@ namespace {
 constexpr int kDecMaxQ = 8;     // query rows per call
 constexpr int kDecWaves = 4;    // waves per work-group
 constexpr int kDecTarget = 512;    // work-groups a split plan aims for (two per CU, one round)
-constexpr int kMergeMax = 4096;    // splits per (head, query) the merge takes
+constexpr int kMergeMax = kDecTarget;  // splits per (head, query) the merge takes
+constexpr int kMaxResidue = 4096;       // classes of the largest residue basis a cache may use
 
 typedef uint32_t du4 __attribute__((ext_vector_type(4)));
 
@@ -38,8 +40,8 @@ struct DecK {
   char* k;  // the cache (written only for the rows this call appends)
   char* v;
   int64_t c_sb, c_sn;  // elements
-  int64_t qpos0, length, Q, chunk;
-  int32_t nq, s, per_class, n_split;
+  int64_t qpos0, length, Q, groups;  // groups: group numbers per class (see plan_of)
+  int32_t nq, s, n_split;             // n_split: work-groups per head
   float c;  // scale * log2(e)
   Pred pred;
   float* o_part;    // [BH][n_split][nq][D]
@@ -118,7 +120,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 // One work-group per (split, head).  Lane l of wave w scores key b0 + l of each block
-// b0 = 256 (jc + r per_class) + 64 w from its K row; the V rows of the block's live keys
+// b0 = 256 k + 64 w of the groups (class, k) the split takes, from its K row; the V rows of the block's live keys
 // go by LDS DMA into the wave's 64-row buffer, and for P.V the lanes own output
 // dimensions (D / 64 each).  MQ = 1 is the single-query case (fewer registers), MQ = kDecMaxQ
 // takes 2..8 queries.
@@ -152,16 +154,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
   }
   __syncthreads();
 
-  // this split's keys: the groups of 256 entries jc, jc + per_class, jc + 2 per_class, ...
-  // of class cls's segment (a.chunk = 256 per_class entries apart), one 64-key block per
-  // wave and group, so that a run of live keys is spread over the class's work-groups
-  const int cls = split / a.per_class;
-  const int64_t jc = split - (int64_t)cls * a.per_class;
-  const int64_t cnt = a.length > cls ? (a.length - 1 - cls) / a.s + 1 : 0;
-  const int64_t i0 = jc * 256;
-  const int64_t i1 = cnt;
-  const char* kseg = a.k + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
-  const char* vseg = a.v + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
+  // this split's keys: the head's segments are cut into groups of 256 entries, numbered
+  // g = class * groups + k (entries 256 k .. 256 k + 255 of the class's segment; a number
+  // past the segment's end is an empty group), and the split takes the groups split,
+  // split + n_split, split + 2 n_split, ..., one 64-key block per wave and group.  A run of
+  // live keys (a window at the end of the context, or the one class that holds a lattice
+  // row's keys) is thus spread over many work-groups, and so are the groups at one place k
+  // of every class (groups and n_split have no common factor).
+  const uint32_t n_groups = (uint32_t)(a.s * a.groups);
   const int64_t rowb = a.c_sn * ESZ;
   const char* knew = a.n_new ? a.k_new + bh * a.new_sb : nullptr;
   const char* vnew = a.n_new ? a.v_new + bh * a.new_sb : nullptr;
@@ -173,11 +173,12 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
   for (int64_t j = 0; j < a.n_new; ++j) {
     const int64_t t = a.new_pos0 + j;
     const int64_t e = t / a.s;
-    if (t - e * a.s != cls || (e >> 8) % a.per_class != jc) continue;
+    const int64_t ncls = t - e * a.s;
+    if ((ncls * a.groups + (e >> 8)) % a.n_split != split) continue;
     if (tid < 2 * NC) {
       const int uu = tid % NC;
       const char* src = (tid < NC ? knew : vnew) + j * a.new_sn + 16 * uu;
-      char* dst = (tid < NC ? a.k : a.v) + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ + e * rowb + 16 * uu;
+      char* dst = (tid < NC ? a.k : a.v) + (bh * a.c_sb + ncls * a.Q * a.c_sn) * ESZ + e * rowb + 16 * uu;
       *reinterpret_cast<du4*>(dst) = *reinterpret_cast<const du4*>(src);
     }
   }
@@ -191,7 +192,13 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
     for (int d = 0; d < DPL; ++d) o[i][d] = 0.f;
   }
 
-  for (int64_t b0 = i0 + 64 * w; b0 < i1; b0 += a.chunk) {
+  for (uint32_t g = (uint32_t)split; g < n_groups; g += (uint32_t)a.n_split) {
+    const int cls = (int)(g / (uint32_t)a.groups);
+    const int64_t b0 = (int64_t)(g - (uint32_t)cls * (uint32_t)a.groups) * 256 + 64 * w;
+    const int64_t i1 = a.length > cls ? (a.length - 1 - cls) / a.s + 1 : 0;  // entries of the class
+    if (b0 >= i1) continue;
+    const char* kseg = a.k + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
+    const char* vseg = a.v + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
     const int64_t idx = b0 + lane;
     const int32_t t = (int32_t)(idx * a.s + cls);  // original position of this lane's key
     uint32_t lv = 0u;                              // bit i: (query i, key) is live
@@ -425,27 +432,29 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const char* k_new, const
 }
 
 struct Plan {
-  int32_t s, per_class, n_split;
-  int64_t chunk, Q;
+  int32_t s, n_split;
+  int64_t groups, Q;
 };
 
-// Split of the keys: per_class work-groups per class's segment, about kDecTarget in all
-// and at most one per 256-key group; work-group j of a class takes groups j, j +
-// per_class, ... (chunk = the stride between them in entries).
+// Split of the keys: each class's segment in groups of 256 entries, the groups of a head
+// numbered class-major and dealt round-robin to n_split work-groups per head, about
+// kDecTarget work-groups in all and at most one per group that holds entries.  With s > 1
+// a class takes `groups` numbers, at least as many as the longest segment needs and with
+// no factor in common with n_split (the surplus numbers are empty groups), so the groups at
+// one place of every class, such as a window's last entries, go to different work-groups.
+// n_split <= kDecTarget = kMergeMax, the splits the merge holds in LDS.
 Plan plan_of(int64_t BH, int64_t capacity, int64_t length, int32_t residue_s) {
   Plan p;
   p.s = residue_s > 1 ? residue_s : 1;
   p.Q = capacity / p.s;
   const int64_t cnt_max = (length + p.s - 1) / p.s;
-  int64_t per = (kDecTarget + BH * p.s - 1) / (BH * p.s);
-  const int64_t groups = (cnt_max + 255) / 256;
-  if (per > groups) per = groups;
-  if (per < 1) per = 1;
-  // the merge holds one weight per split in LDS (terminates: s <= kMergeMax is checked)
-  while (per > 1 && p.s * per > kMergeMax) per = (per + 1) / 2;
-  p.per_class = (int32_t)(cnt_max > 0 ? per : 0);
-  p.chunk = per * 256;
-  p.n_split = p.s * p.per_class;
+  const int64_t need = (cnt_max + 255) / 256;
+  int64_t per = (kDecTarget + BH - 1) / BH;
+  if (per > p.s * need) per = p.s * need;
+  p.n_split = (int32_t)per;
+  p.groups = need;
+  if (p.s > 1 && per > 1)
+    while (std::gcd(p.groups, per) != 1) ++p.groups;  // ends within per steps (per and per+1 are coprime)
   return p;
 }
 
@@ -457,8 +466,7 @@ int check_decode(const pa_decode_args* x) {
   PA_CHECK_ARG(x->D == 128 || x->D == 64, "pa_decode: D=%d (64 or 128)", x->D);
   PA_CHECK_ARG(x->dtype != PA_F32 || x->D == 64, "pa_decode: float32 needs D = 64");
   const int32_t s = x->residue_s > 1 ? x->residue_s : 1;
-  // the merge holds one weight per split and every class is at least one split
-  PA_CHECK_ARG(s <= kMergeMax, "pa_decode: residue_s=%d exceeds %d classes", s, kMergeMax);
+  PA_CHECK_ARG(s <= kMaxResidue, "pa_decode: residue_s=%d exceeds %d classes", s, kMaxResidue);
   PA_CHECK_ARG(x->capacity >= 1 && x->capacity < (1ll << 31) && x->capacity % s == 0,
                "pa_decode: capacity=%lld must be in 1..2^31-1 and a multiple of s=%d", (long long)x->capacity, s);
   PA_CHECK_ARG(x->length >= 0 && x->length <= x->capacity, "pa_decode: length=%lld outside 0..capacity",
@@ -597,10 +605,9 @@ int decode_launch(const pa_decode_args* x, const Plan& p, float* ws, hipStream_t
   k.qpos0 = x->qpos0;
   k.length = x->length;
   k.Q = p.Q;
-  k.chunk = p.chunk;
+  k.groups = p.groups;
   k.nq = x->nq;
   k.s = p.s;
-  k.per_class = p.per_class;
   k.n_split = p.n_split;
   k.c = (x->scale > 0.f ? x->scale : 1.f / sqrtf((float)x->D)) * 1.4426950408889634f;
   k.pred = pa::make_pred(x->mask);
@@ -647,7 +654,7 @@ extern "C" int pa_kv_append(const void* k_new, const void* v_new, int64_t new_sb
                             int32_t dtype, int64_t capacity, int64_t pos0, int32_t residue_s, void* stream) {
   PA_CHECK_ARG(dtype == PA_BF16 || dtype == PA_F16 || dtype == PA_F32, "pa_kv_append: dtype %d", dtype);
   const int64_t s = residue_s > 1 ? residue_s : 1;
-  PA_CHECK_ARG(s <= pa::kMergeMax, "pa_kv_append: residue_s=%d exceeds %d classes", residue_s, pa::kMergeMax);
+  PA_CHECK_ARG(s <= pa::kMaxResidue, "pa_kv_append: residue_s=%d exceeds %d classes", residue_s, pa::kMaxResidue);
   PA_CHECK_ARG(BH >= 1 && n >= 0 && D >= 1, "pa_kv_append: BH=%lld n=%lld D=%d", (long long)BH, (long long)n, D);
   PA_CHECK_ARG(capacity >= 1 && capacity % s == 0, "pa_kv_append: capacity=%lld not a multiple of s=%lld",
                (long long)capacity, (long long)s);

@@ -50,7 +50,7 @@ class DecodeLaunch:
         return self.out
 
 
-# the decode merge holds one weight per split, and every residue class is one split at least
+# classes of the largest residue basis a cache may use (the library's limit too)
 MAX_CLASSES = 4096
 
 
@@ -60,7 +60,7 @@ class KVCache:
     def __init__(self, BH, capacity, D, dtype=torch.bfloat16, residue=0, device=None):
         s = int(residue) if residue and residue > 1 else 1
         if s > MAX_CLASSES:
-            raise ValueError(f"residue={residue}: the decode merge takes at most {MAX_CLASSES} classes")
+            raise ValueError(f"residue={residue}: a cache's basis has at most {MAX_CLASSES} classes")
         if capacity < 1 or capacity % s:
             raise ValueError(f"capacity={capacity} must be a positive multiple of the residue stride {s}")
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())

@@ -179,8 +179,9 @@ def test_backward_host_checks_on_lse_layout():
             plan.backward(q, q, q, q, lse, q)
 
 
-def test_decode_rejects_more_residue_classes_than_the_merge_takes():
-    """residue_s > 4096 left the split planner without an exit; it is an argument error."""
+def test_decode_rejects_residue_bases_beyond_4096_classes():
+    """A cache's basis has at most 4096 classes (an earlier split planner had no exit past
+    that); a larger residue_s is an argument error."""
     lib = _lib.lib()
     a = _lib.PaDecodeArgs()
     buf = (ctypes.c_int64 * 64)()
