@@ -108,6 +108,11 @@ __device__ __forceinline__ void lds_dma16(uint32_t m0, const char* gbase, uint32
                : "m0");
 }
 
+// The same from a 64-bit address per lane.
+__device__ __forceinline__ void lds_dma16_va(uint32_t m0, const char* p) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(p) : "m0");
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
@@ -119,12 +124,13 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// One work-group per (split, head).  Lane l of wave w scores key b0 + l of each block
-// b0 = 256 k + 64 w of the groups (class, k) the split takes, from its K row; the V rows of the block's live keys
-// go by LDS DMA into the wave's 64-row buffer, and for P.V the lanes own output
-// dimensions (D / 64 each).  MQ = 1 is the single-query case (fewer registers), MQ = kDecMaxQ
-// takes 2..8 queries.
-template <typename T, int D, int MQ>
+// One work-group per (split, head).  Wave w takes the blocks b0 = 256 k + 64 w of the
+// groups (class, k) the split takes.  LIST: it lists the blocks' live keys, then, 64 listed
+// keys at a time, lane l scores key l from its K row; else lane l scores key b0 + l of each
+// block that holds a live key.  The keys' V rows go by LDS DMA into the wave's 64-row
+// buffer, and for P.V the lanes own output dimensions (D / 64 each).  MQ = 1 is the
+// single-query case (fewer registers), MQ = kDecMaxQ takes 2..8 queries.
+template <typename T, int D, int MQ, bool LIST>
 __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
   constexpr int ESZ = sizeof(T);
   constexpr int RB = D * ESZ;     // row bytes
@@ -137,6 +143,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
   __shared__ __attribute__((aligned(16))) char q_lds[MQ * RB];
   __shared__ float red_m[kDecWaves][MQ];
   __shared__ float red_l[kDecWaves][MQ];
+  __shared__ int32_t kl_row[kDecWaves][128];  // each wave's list of live keys
+  __shared__ uint32_t kl_lv[kDecWaves][128];
   static_assert(sizeof(float) * kDecWaves * MQ * D <= sizeof(vbuf), "partials fit the V buffers");
   float(*red_o)[MQ][D] = reinterpret_cast<float(*)[MQ][D]>(vbuf);
 
@@ -192,61 +200,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
     for (int d = 0; d < DPL; ++d) o[i][d] = 0.f;
   }
 
-  for (uint32_t g = (uint32_t)split; g < n_groups; g += (uint32_t)a.n_split) {
-    const int cls = (int)(g / (uint32_t)a.groups);
-    const int64_t b0 = (int64_t)(g - (uint32_t)cls * (uint32_t)a.groups) * 256 + 64 * w;
-    const int64_t i1 = a.length > cls ? (a.length - 1 - cls) / a.s + 1 : 0;  // entries of the class
-    if (b0 >= i1) continue;
-    const char* kseg = a.k + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
-    const char* vseg = a.v + (bh * a.c_sb + (int64_t)cls * a.Q * a.c_sn) * ESZ;
-    const int64_t idx = b0 + lane;
-    const int32_t t = (int32_t)(idx * a.s + cls);  // original position of this lane's key
-    uint32_t lv = 0u;                              // bit i: (query i, key) is live
-    if (idx < i1) {
-#pragma unroll
-      for (int i = 0; i < MQ; ++i)
-        if (i < nq && pred_live(a.pred, (int32_t)(a.qpos0 + i), t)) lv |= 1u << i;
-    }
-    const uint64_t any = __ballot(lv != 0u);
-    if (any == 0ull) continue;
-    // keys appended by this call: read from k_new / v_new
-    const int64_t jn = (int64_t)t - a.new_pos0;
-    const bool isnew = idx < i1 && jn >= 0 && jn < a.n_new;
-    const uint64_t newm = a.n_new ? __ballot(isnew) : 0ull;
+  const char* kh = a.k + bh * a.c_sb * ESZ;
+  const char* vh = a.v + bh * a.c_sb * ESZ;
+  const uint32_t vbw = (uint32_t)(uintptr_t)(vbuf + w * 64 * RB);
+  const char* vbuf_w = vbuf + w * 64 * RB;
 
-    // the V rows of the keys live for some query, into this wave's buffer (lanes of a dead
-    // row are masked off; a DMA instruction whose rows are all dead is skipped), and the
-    // K row of each live key, one per lane, all in flight together
-    const char* vblk = vseg + b0 * rowb;
-    const uint32_t vbw = (uint32_t)(uintptr_t)(vbuf + w * 64 * RB);
-#pragma unroll
-    for (int r = 0; r < 64 / RPI; ++r) {
-      if ((any >> (r * RPI)) & ((1ull << RPI) - 1ull)) {
-        const int row = r * RPI + lane / LPR;
-        if (((any & ~newm) >> row) & 1ull)
-          lds_dma16(vbw + r * 1024, vblk, (uint32_t)(row * rowb + 16 * (lane % LPR)));
-      }
-    }
-    if (newm & any) {
-      // an appended row's 16-byte units, from v_new into the same place of the buffer
-#pragma unroll
-      for (int r = 0; r < 64 / RPI; ++r) {
-        const int row = r * RPI + lane / LPR;
-        if (((newm & any) >> row) & 1ull) {
-          const int64_t jr = ((b0 + row) * a.s + cls) - a.new_pos0;
-          *reinterpret_cast<du4*>(vbuf + w * 64 * RB + r * 1024 + 16 * lane) =
-              *reinterpret_cast<const du4*>(vnew + jr * a.new_sn + 16 * (lane % LPR));
-        }
-      }
-    }
-    du4 kr[NC];
-#pragma unroll
-    for (int cc = 0; cc < NC; ++cc) kr[cc] = du4{0u, 0u, 0u, 0u};
-    if (lv) {
-      const char* kp = isnew ? knew + jn * a.new_sn : kseg + idx * rowb;
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc) kr[cc] = *reinterpret_cast<const du4*>(kp + 16 * cc);
-    }
+  // A batch of up to 64 keys, lane l holding key l's K row (kr) and live bits (lv), their V
+  // rows in the buffer rows set in bmask (in flight by DMA): scores, online softmax, P.V.
+  auto consume = [&](const du4(&kr)[NC], uint32_t lv, uint64_t bmask) {
     float p[MQ];
 #pragma unroll
     for (int i = 0; i < MQ; ++i) {
@@ -269,14 +230,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
         }
       }
     }
-    // P.V over the live keys, V from the buffer (this wave's own DMA: waiting for it is enough)
+    // P.V, V from the buffer (this wave's own DMA: waiting for it is enough)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const char* vrow = vbuf + w * 64 * RB + lane * DPL * ESZ;
-    // eight keys at a time: their buffer rows are read together (a dead key's row holds
+    const char* vrow = vbuf_w + lane * DPL * ESZ;
+    // eight rows at a time: their buffer rows are read together (a row outside bmask holds
     // stale data and is read but not used), so the reads' latency is paid once per eight
 #pragma unroll
     for (int u0 = 0; u0 < 64; u0 += 8) {
-      const uint32_t bits8 = (uint32_t)(any >> u0) & 0xffu;
+      const uint32_t bits8 = (uint32_t)(bmask >> u0) & 0xffu;
       if (bits8 == 0u) continue;
       uint32_t vw[8];
 #pragma unroll
@@ -305,6 +266,155 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecK a) {
       }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // buffer reads done before the next DMA
+  };
+
+  if constexpr (LIST) {
+    // The wave scans its blocks' keys for liveness and lists the live ones in LDS (kl_row:
+    // the key's row in the head's cache, or -1 - j for the call's appended token j; kl_lv:
+    // bit i set when the key is live for query i), then takes them 64 at a time: a block
+    // with a few live keys costs its scan, not a round trip to memory.
+    int nlist = 0;  // entries in the wave's list (at most 63 + 64)
+    uint32_t g = (uint32_t)split;
+    while (true) {
+      while (nlist < 64 && g < n_groups) {
+        const int cls = (int)(g / (uint32_t)a.groups);
+        const int64_t b0 = (int64_t)(g - (uint32_t)cls * (uint32_t)a.groups) * 256 + 64 * w;
+        const int64_t i1 = a.length > cls ? (a.length - 1 - cls) / a.s + 1 : 0;  // entries of the class
+        g += (uint32_t)a.n_split;
+        if (b0 >= i1) continue;
+        const int64_t idx = b0 + lane;
+        const int32_t t = (int32_t)(idx * a.s + cls);  // original position of this lane's key
+        uint32_t bits = 0u;
+        if (idx < i1) {
+#pragma unroll
+          for (int i = 0; i < MQ; ++i)
+            if (i < nq && pred_live(a.pred, (int32_t)(a.qpos0 + i), t)) bits |= 1u << i;
+        }
+        const uint64_t any = __ballot(bits != 0u);
+        if (any == 0ull) continue;
+        if (bits) {
+          const int pos = nlist + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(any >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)any, 0u));
+          const int64_t jn = (int64_t)t - a.new_pos0;
+          kl_row[w][pos] = (jn >= 0 && jn < a.n_new) ? (int32_t)(-1 - jn) : (int32_t)(cls * a.Q + idx);
+          kl_lv[w][pos] = bits;
+        }
+        nlist += (int)__builtin_popcountll(any);
+      }
+      if (nlist == 0) break;
+      const int nb = nlist < 64 ? nlist : 64;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the list's entries are written
+      int32_t code = 0;
+      uint32_t lv = 0u;
+      if (lane < nb) {
+        code = kl_row[w][lane];
+        lv = kl_lv[w][lane];
+      }
+      // the entries' V rows into buffer rows 0..nb-1 (RPI rows per DMA instruction, each
+      // lane's row code read from the list; an appended row's 16-byte units from v_new),
+      // and each entry's K row, one per lane, all in flight together
+      const uint64_t newm = a.n_new ? __ballot(lane < nb && code < 0) : 0ull;
+#pragma unroll
+      for (int r = 0; r < 64 / RPI; ++r) {
+        const int e = r * RPI + lane / LPR;
+        const int32_t ce = kl_row[w][e];  // (past nb: not used)
+        if (r * RPI < nb && e < nb && ce >= 0)
+          lds_dma16_va(vbw + r * 1024, vh + (int64_t)ce * rowb + 16 * (lane % LPR));
+      }
+      if (newm) {
+#pragma unroll
+        for (int r = 0; r < 64 / RPI; ++r) {
+          const int e = r * RPI + lane / LPR;
+          const int32_t ce = __shfl(code, e);  // (every lane takes part in the shuffle)
+          if ((newm >> e) & 1ull)
+            *reinterpret_cast<du4*>(vbuf + w * 64 * RB + r * 1024 + 16 * lane) =
+                *reinterpret_cast<const du4*>(vnew + (int64_t)(-1 - ce) * a.new_sn + 16 * (lane % LPR));
+        }
+      }
+      du4 kr[NC];
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) kr[cc] = du4{0u, 0u, 0u, 0u};
+      if (lane < nb) {
+        const char* kp = code >= 0 ? kh + (int64_t)code * rowb : knew + (int64_t)(-1 - code) * a.new_sn;
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) kr[cc] = *reinterpret_cast<const du4*>(kp + 16 * cc);
+      }
+      consume(kr, lv, nb == 64 ? ~0ull : ((1ull << nb) - 1ull));
+      // the list's entries past the batch move to its front
+      nlist -= nb;
+      if (nlist > 0) {
+        int32_t r2 = 0;
+        uint32_t l2 = 0u;
+        if (lane < nlist) {
+          r2 = kl_row[w][64 + lane];
+          l2 = kl_lv[w][64 + lane];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane < nlist) {
+          kl_row[w][lane] = r2;
+          kl_lv[w][lane] = l2;
+        }
+      }
+    }
+  } else {
+    // block by block: lane l scores key b0 + l of each of the wave's blocks that holds a
+    // live key
+    for (uint32_t g = (uint32_t)split; g < n_groups; g += (uint32_t)a.n_split) {
+      const int cls = (int)(g / (uint32_t)a.groups);
+      const int64_t b0 = (int64_t)(g - (uint32_t)cls * (uint32_t)a.groups) * 256 + 64 * w;
+      const int64_t i1 = a.length > cls ? (a.length - 1 - cls) / a.s + 1 : 0;  // entries of the class
+      if (b0 >= i1) continue;
+      const char* kseg = kh + (int64_t)cls * a.Q * rowb;
+      const char* vseg = vh + (int64_t)cls * a.Q * rowb;
+      const int64_t idx = b0 + lane;
+      const int32_t t = (int32_t)(idx * a.s + cls);  // original position of this lane's key
+      uint32_t lv = 0u;  // bit i: (query i, key) is live
+      if (idx < i1) {
+#pragma unroll
+        for (int i = 0; i < MQ; ++i)
+          if (i < nq && pred_live(a.pred, (int32_t)(a.qpos0 + i), t)) lv |= 1u << i;
+      }
+      const uint64_t any = __ballot(lv != 0u);
+      if (any == 0ull) continue;
+      // keys appended by this call: read from k_new / v_new
+      const int64_t jn = (int64_t)t - a.new_pos0;
+      const bool isnew = idx < i1 && jn >= 0 && jn < a.n_new;
+      const uint64_t newm = a.n_new ? __ballot(isnew) : 0ull;
+
+      // the V rows of the keys live for some query, into this wave's buffer (lanes of a
+      // dead row are masked off; a DMA instruction whose rows are all dead is skipped),
+      // and the K row of each live key, one per lane, all in flight together
+      const char* vblk = vseg + b0 * rowb;
+#pragma unroll
+      for (int r = 0; r < 64 / RPI; ++r) {
+        if ((any >> (r * RPI)) & ((1ull << RPI) - 1ull)) {
+          const int row = r * RPI + lane / LPR;
+          if (((any & ~newm) >> row) & 1ull)
+            lds_dma16(vbw + r * 1024, vblk, (uint32_t)(row * rowb + 16 * (lane % LPR)));
+        }
+      }
+      if (newm & any) {
+        // an appended row's 16-byte units, from v_new into the same place of the buffer
+#pragma unroll
+        for (int r = 0; r < 64 / RPI; ++r) {
+          const int row = r * RPI + lane / LPR;
+          if (((newm & any) >> row) & 1ull) {
+            const int64_t jr = ((b0 + row) * a.s + cls) - a.new_pos0;
+            *reinterpret_cast<du4*>(vbuf + w * 64 * RB + r * 1024 + 16 * lane) =
+                *reinterpret_cast<const du4*>(vnew + jr * a.new_sn + 16 * (lane % LPR));
+          }
+        }
+      }
+      du4 kr[NC];
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) kr[cc] = du4{0u, 0u, 0u, 0u};
+      if (lv) {
+        const char* kp = isnew ? knew + jn * a.new_sn : kseg + idx * rowb;
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) kr[cc] = *reinterpret_cast<const du4*>(kp + 16 * cc);
+      }
+      consume(kr, lv, any);
+    }
   }
   __syncthreads();  // every wave is past its buffer: it now holds the partials
 
@@ -498,13 +608,23 @@ int check_decode(const pa_decode_args* x) {
   return PA_OK;
 }
 
+// The identity basis takes the kernel's key list (live keys spread thinly over many
+// blocks); a residue basis, whose relabelling gathers the live keys into few full blocks,
+// takes block by block.
 template <typename T, int D>
 int launch_decode(const DecK& k, int64_t BH, hipStream_t s) {
-  if (k.nq == 1)
-    hipLaunchKernelGGL((decode_kernel<T, D, 1>), dim3((unsigned)k.n_split, (unsigned)BH), dim3(256), 0, s, k);
-  else
-    hipLaunchKernelGGL((decode_kernel<T, D, kDecMaxQ>), dim3((unsigned)k.n_split, (unsigned)BH), dim3(256), 0, s,
-                       k);
+  const dim3 grid((unsigned)k.n_split, (unsigned)BH);
+  if (k.nq == 1) {
+    if (k.s == 1)
+      hipLaunchKernelGGL((decode_kernel<T, D, 1, true>), grid, dim3(256), 0, s, k);
+    else
+      hipLaunchKernelGGL((decode_kernel<T, D, 1, false>), grid, dim3(256), 0, s, k);
+  } else {
+    if (k.s == 1)
+      hipLaunchKernelGGL((decode_kernel<T, D, kDecMaxQ, true>), grid, dim3(256), 0, s, k);
+    else
+      hipLaunchKernelGGL((decode_kernel<T, D, kDecMaxQ, false>), grid, dim3(256), 0, s, k);
+  }
   PA_LAUNCH_CHECK("decode_kernel");
   return PA_OK;
 }
