@@ -106,6 +106,30 @@ def test_dead_queries_and_empty_cache(gpu):
     check_close(out[:, :1], want, torch.bfloat16, "dense mask decode")
 
 
+@pytest.mark.parametrize("residue", [0, 16])
+@pytest.mark.parametrize("nq", [1, 3])
+def test_decode_with_many_live_keys_per_block(gpu, residue, nq):
+    """64 heads, so each of a head's 8 work-groups takes 2 groups of 256 keys and each wave
+    two 64-key blocks; every block holds about 45 keys live for some query (a random mask
+    of density 0.7), so in the identity basis a wave's list of live keys passes 64 and the
+    rest carries over to a second batch.  Against the oracle on every head."""
+    BH, cap, D = 64, 4096, 128
+    L = cap
+    q, k, v = make_qkv(BH, cap, D, torch.bfloat16, seed=7 + nq)
+    rng = np.random.default_rng(11 + nq)
+    M = np.zeros((cap, cap), dtype=bool)
+    qpos0 = L - nq
+    M[qpos0:L, :L] = rng.random((nq, L)) < 0.7
+    cache = pdec.KVCache(BH, cap, D, torch.bfloat16, residue, gpu)
+    _fill(cache, k, v, [L - 100, 100], gpu)
+    lse = torch.empty(BH, nq, device=gpu)
+    out = cache.attend(q[:, qpos0:L].to(gpu), pm.DenseMask(M), lse=lse)
+    want, want_lse = oatt.dense_attention(as64(q[:, qpos0:L]), as64(k[:, :L]), as64(v[:, :L]),
+                                          lambda r0, r1: M[qpos0 + r0:qpos0 + r1, :L])
+    check_close(out, want, torch.bfloat16, f"decode dense-random s={residue} nq={nq}")
+    assert np.abs(lse.cpu().numpy() - want_lse).max() < 2e-2
+
+
 def test_bases_agree_at_the_headline_size(gpu):
     """band-256 | lattice-16, L = 16384, 32 heads, D = 128: the newest token decoded in the
     identity and the rp16 basis; both against the oracle on two heads."""
