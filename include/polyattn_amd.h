@@ -313,8 +313,9 @@ int pa_lse_merge(const float* const* o_parts, const float* const* lse_parts, int
  * arrive in original order and would have to be inserted at permuted positions
  * (docs/NOTES.md:2145-2153, 2201-2203).  These entry points answer it for the residue
  * bases of gpu/permute.py:12-15.  A cache of `capacity` rows per head (a multiple of
- * s; s = residue_s, 0 or 1 = identity) keeps the token at original position t at row
- * (t mod s) * (capacity / s) + t div s, so appending never moves a cached row.
+ * s; s = residue_s, 0 or 1 = identity, at most 4096) keeps the token at original
+ * position t at row (t mod s) * (capacity / s) + t div s, so appending never moves a
+ * cached row.
  *
  * pa_kv_append: rows j = 0..n-1 of k_new / v_new [BH, n, D] (strides in elements) are
  * the tokens at original positions pos0 + j; each is written to its basis row of
