@@ -179,6 +179,39 @@ def test_backward_host_checks_on_lse_layout():
             plan.backward(q, q, q, q, lse, q)
 
 
+@pytest.mark.parametrize("BH,cap,length,s,splits", [
+    (32, 16384, 16384, 16, 16),   # 4 groups per class, 16 classes: 16 work-groups per head
+    (32, 16384, 16384, 0, 16),    # identity: 64 groups, 512 / 32 work-groups per head
+    (1, 16384, 16384, 0, 64),     # one head: a work-group per group
+    (8, 65536, 65536, 32, 64),
+    (64, 4096, 4000, 16, 8),
+    (3, 1024, 1, 16, 16),         # one entry: every class is one (mostly empty) group
+    (2, 2048, 0, 8, 0),           # empty cache: no split launch
+    (65535, 256, 256, 0, 1),
+])
+def test_decode_split_plan(BH, cap, length, s, splits):
+    """The decode split plan, read back through pa_decode_workspace (BH * splits * nq *
+    (D + 1) floats): about 512 work-groups in all, never more per head than there are
+    256-entry groups, none for an empty cache."""
+    lib = _lib.lib()
+    a = _lib.PaDecodeArgs()
+    buf = (ctypes.c_int64 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    a.q, a.k_cache, a.v_cache, a.o = p, p, p, p
+    a.nq, a.BH, a.D, a.dtype = 1, BH, 128, _lib.PA_BF16
+    a.q_sb, a.q_sn, a.c_sb, a.c_sn, a.o_sb, a.o_sn = 128, 128, cap * 128, 128, 128, 128
+    a.capacity, a.length, a.residue_s = cap, length, s
+    a.mask.n_include = 1
+    n = ctypes.c_int64(-1)
+    assert lib.pa_decode_workspace(ctypes.byref(a), ctypes.byref(n)) == _lib.PA_OK
+    assert n.value % (BH * 129 * 4) == 0
+    got = n.value // (BH * 129 * 4)
+    assert got == splits
+    classes = max(s, 1)
+    groups = classes * -(-(-(-length // classes)) // 256)   # 256-entry groups of the head
+    assert got <= min(512, groups)
+
+
 def test_decode_rejects_residue_bases_beyond_4096_classes():
     """A cache's basis has at most 4096 classes (an earlier split planner had no exit past
     that); a larger residue_s is an argument error."""
