@@ -637,6 +637,8 @@ def main():
                     help="only copy a MIB-sized device buffer a few times (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
     a = ap.parse_args()
+    if a.steps < 1 or a.warmup < 0:
+        ap.error(f"--steps must be >= 1 and --warmup >= 0 (got {a.steps}, {a.warmup})")
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}). "
               "The attention shards over heads with no exchange; run one process per GPU.", file=sys.stderr)
