@@ -148,6 +148,32 @@ def test_bases_agree_at_the_headline_size(gpu):
     assert (outs[0] - outs[1]).abs().max().item() < 2e-2
 
 
+@pytest.mark.parametrize("name,s", [("bandlat-L16k", 16), ("sinkwin-L32k", 16), ("dilated8-L8k", 8),
+                                    ("prefixlat-L64k", 32)])
+@pytest.mark.parametrize("basis", ["identity", "residue"])
+def test_decode_step_at_each_workload_size(gpu, name, s, basis):
+    """The bench's decode step at the workload's full size: the newest token's K / V appended
+    and its query attended in one call, against the float64 oracle on the first and last
+    head (the whole mask's row of the newest token)."""
+    from polyhedral_amd import workloads
+    wl = workloads.make(name)
+    H, L, D = wl.H, wl.L, wl.D
+    q, k, v = wl.inputs(0, gpu)
+    cache = pdec.KVCache(H, L, D, q.dtype, s if basis == "residue" else 0, gpu)
+    cache.append(k[:, :L - 1], v[:, :L - 1])
+    lse = torch.empty(H, 1, device=gpu)
+    out = cache.attend(q[:, L - 1:].contiguous(), wl.union, lse=lse,
+                       k_new=k[:, L - 1:].contiguous(), v_new=v[:, L - 1:].contiguous())
+    torch.cuda.synchronize()
+    live = np.asarray(wl.union.row_cols(L - 1, L), dtype=bool)
+    heads = [0, H - 1]
+    want, want_lse = oatt.dense_attention(as64(q[heads, L - 1:]), as64(k[heads]), as64(v[heads]),
+                                          lambda r0, r1: live[None])
+    check_close(out[heads], want, q.dtype, f"decode step {name} {basis}")
+    assert np.abs(lse[heads].cpu().numpy() - want_lse).max() < 2e-2
+    del cache, q, k, v
+
+
 @pytest.mark.parametrize("static", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("residue", [0, 16])
