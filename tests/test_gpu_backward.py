@@ -239,15 +239,17 @@ def test_headline_size_split_equals_one_basis(gpu):
         assert err < 2e-2, f"{nm}: split and one-basis backwards differ by {err:.3e} (relative to the largest)"
 
 
-def test_headline_size_sampled_gradients_equal_oracle(gpu):
-    """band-256 | lattice-16 at L = 16384, H = 32, D = 128: the split backward's dQ on
-    sampled query rows, and dK / dV on sampled keys near the end of the sequence, against
-    the float64 oracle on heads 0 and H - 1.  The oracle's rows are independent, so dQ of
-    a row needs only that row, and dK / dV of a key need only the query rows live for it
-    (its band rows and its lattice rows after it, a few hundred for these keys)."""
+@pytest.mark.parametrize("name", ["bandlat-L16k", "sinkwin-L32k", "dilated8-L8k", "prefixlat-L64k"])
+def test_workload_size_sampled_gradients_equal_oracle(gpu, name):
+    """Each bf16 workload at its full size (the headline band-256 | lattice-16 at L = 16384,
+    H = 32 among them): the split backward's dQ on sampled query rows, and dK / dV on
+    sampled keys near the end of the sequence, against the float64 oracle on the first and
+    last head.  The oracle's rows are independent, so dQ of a row needs only that row, and
+    dK / dV of a key need only the query rows live for it (the masks are causal, so those
+    rows come after the key)."""
     from polyhedral_amd import workloads
     from polyhedral_amd.split import SplitPlan
-    wl = workloads.make("bandlat-L16k")
+    wl = workloads.make(name)
     L = wl.L
     q, k, v = wl.inputs(0, gpu)
     launches, o, lse = SplitPlan(wl.pieces, L, gpu).prepare(q, k, v)
@@ -261,24 +263,23 @@ def test_headline_size_sampled_gradients_equal_oracle(gpu):
     def row_mask(rows):
         return np.stack([np.asarray(wl.union.row_cols(int(i), L), dtype=bool) for i in rows])
 
+    keys = np.array([L - 1, L - 20, L - 100])
+    span = np.arange(L - 400, L)
+    cols = row_mask(span)[:, keys]
+    qrows = span[cols.any(axis=1)]
+    # (no row before the span sees these keys)
+    assert not np.asarray(wl.union.row_cols(L - 401, L), dtype=bool)[keys.min():].any()
+    rows = np.array([0, 1, 255, 256, L // 2 + 1, L - 2, L - 1])
     for h in (0, wl.H - 1):
         kh, vh = as64(k[h:h + 1]), as64(v[h:h + 1])
-        # dQ of sampled rows
-        rows = np.array([0, 1, 255, 256, 4097, 8191, 12345, L - 1])
         M = row_mask(rows)
         want_dq, _, _ = oatt.dense_attention_bwd(as64(q[h:h + 1, rows]), kh, vh, as64(do[h:h + 1, rows]),
                                                   lambda r0, r1: M[r0:r1])
         e = _rel_err(dq[h:h + 1, rows], want_dq)
-        assert e < REL[torch.bfloat16], f"head {h} dq rows: relative error {e:.3e}"
-        # dK / dV of sampled keys, from every query row live for them
-        keys = np.array([L - 1, L - 50, L - 300])
-        cols = np.stack([np.asarray(wl.union.row_cols(i, L), dtype=bool)[keys] for i in range(L - 600, L)])
-        qrows = np.arange(L - 600, L)[cols.any(axis=1)]
-        # (the mask is causal, so no row before L - 600 sees these keys)
-        assert not np.asarray(wl.union.row_cols(L - 601, L), dtype=bool)[keys.min():].any()
+        assert e < REL[torch.bfloat16], f"{name} head {h} dq rows: relative error {e:.3e}"
         M = row_mask(qrows)
         _, want_dk, want_dv = oatt.dense_attention_bwd(as64(q[h:h + 1, qrows]), kh, vh,
                                                         as64(do[h:h + 1, qrows]), lambda r0, r1: M[r0:r1])
         for g, w_, nm in ((dk, want_dk, "dk"), (dv, want_dv, "dv")):
             e = _rel_err(g[h:h + 1, keys], w_[:, keys])
-            assert e < REL[torch.bfloat16], f"head {h} {nm} keys: relative error {e:.3e}"
+            assert e < REL[torch.bfloat16], f"{name} head {h} {nm} keys: relative error {e:.3e}"
