@@ -39,7 +39,8 @@ PEAK_TFLOPS = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}   # dense MFMA, MI35
 HBM_GBPS = 8000.0
 # oracle predicate name of each workload's whole mask
 ORACLE_NAME = {"window128-L1k": "window-128", "dilated8-L8k": "dilated-8", "bandlat-L16k": "band256+lat16",
-               "sinkwin-L32k": "sinks64+win1024", "prefixlat-L64k": "prefixlm-2048"}
+               "sinkwin-L32k": "sinks64+win1024", "prefixlat-L64k": "prefixlm-2048",
+          "bandlat32-L64k": "band256+lat32"}
 
 
 def log(*a):
@@ -105,6 +106,42 @@ def measure_isolated(plan_launches, reps, flush_mib=512):
         out.append(s.elapsed_time(e))
     del cache
     return statistics.median(out)
+
+
+def measure_graph(plan_launches, steps_per_graph=10, rounds=3, min_ms=50.0):
+    """The device's rate for a forward: `steps_per_graph` forwards captured in one HIP
+    graph and replayed back to back (a forward of a few microseconds is otherwise paced
+    by the host's launches).  Median over `rounds` rounds of replays, each at least
+    `min_ms` long.  Returns ms per forward."""
+    import torch
+    dev = plan_launches[0].device
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for _ in range(steps_per_graph):
+                for launch in plan_launches:
+                    launch()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    per = max(1e-3, (time.perf_counter() - t0) * 1e3)
+    reps = max(1, int(min_ms / per))
+    out = []
+    for _ in range(rounds):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(reps):
+            g.replay()
+        ev[1].record()
+        torch.cuda.synchronize()
+        out.append(ev[0].elapsed_time(ev[1]) / (reps * steps_per_graph))
+    del g
+    return sorted(out)[len(out) // 2]
 
 
 def measure_permute(q, k, v, s, reps=50, warmup=10):
@@ -436,16 +473,23 @@ def settle(launches, min_ms):
             return ms, n
 
 
-def algorithmic_bytes(plan, wl, esz):
-    """Per launch of the plan: Q, K and V rows read once, O and LSE written once; a piece
-    that merges into a previous piece's result also reads that O and LSE once."""
+def algorithmic_bytes(wl, esz):
+    """The problem's algorithmic HBM bytes per forward: Q, K and V read once, O written
+    once (4 x H x L x D elements), whatever the decomposition."""
+    return 4 * wl.H * wl.L * wl.D * esz
+
+
+def split_bytes(plan, wl, esz):
+    """Per launch of the plan, the bytes the decomposition as built must move at least:
+    Q, K and V rows read once, O and LSE written once; a piece that merges into a
+    previous piece's result also reads that O and LSE once.  Above algorithmic_bytes
+    when the plan has several passes (each re-reads Q, K and V, and the merge reads
+    the previous output back)."""
     t = wl.H * wl.L * wl.D * esz
     lse = wl.H * wl.L * 4
     out = []
     first = True
     for pieces in plan.launched:
-        # one launch runs one piece, or both pieces of a split (Q, K, V read and O, LSE
-        # written once; the merge input stays on chip or in cache)
         rd = 3 * t + (t + lse if not first else 0)
         out.append(dict(read=rd, write=t + lse))
         first = False
@@ -491,6 +535,7 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0", extra
     s_ms, s_n = settle(launches, settle_ms)
     wall_ms, per_launch = measure(launches, steps, warmup)
     extras = extras and variant is None
+    graph_ms = measure_graph(launches)
     iso_ms = measure_isolated(launches, max(25, min(steps, 100))) if extras else None
     residues = [b["piece"].residue for b in plan.built if b["piece"].residue]
     permute = measure_permute(q, k, v, residues[0]) if residues and extras else None
@@ -524,9 +569,15 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0", extra
     dt = _dt(wl.dtype)
     peak = PEAK_TFLOPS[dt]
     achieved = flops_live / (kern_ms * 1e-3) / 1e12
-    ab = algorithmic_bytes(plan, wl, q.element_size())
-    nbytes = sum(x["read"] + x["write"] for x in ab)
+    nbytes = algorithmic_bytes(wl, q.element_size())
     bound, inten, ridge, mfma, hbm = roofline(flops_live, nbytes, kern_ms * 1e-3, dt)
+    sb = split_bytes(plan, wl, q.element_size())
+    sbytes = sum(x["read"] + x["write"] for x in sb)
+    split_hbm = dict(bytes=int(sbytes), per_launch=sb,
+                     achieved=round(sbytes / (kern_ms * 1e-3) / 1e9, 1), peak=HBM_GBPS, unit="GB/s",
+                     frac=round(sbytes / (kern_ms * 1e-3) / 1e9 / HBM_GBPS, 4),
+                     note="bytes the decomposition as built must move at least (each pass reads Q, K, V; "
+                          "a merging pass also reads the previous O and LSE), over the kernel time")
     res = dict(
         workload=name + (f"[{variant}]" if variant else ""), description=wl.description, dtype=dt,
         H=wl.H, L=wl.L, D=wl.D, live_pairs_per_head=live, tile_elements_per_head=plan.elements,
@@ -544,10 +595,16 @@ def run(name, steps, warmup, with_cpu=True, variant=None, device="cuda:0", extra
         kernel_live_tflops=round(achieved, 3), tile_tflops=round(flops_tile / (kern_ms * 1e-3) / 1e12, 3),
         peak_tflops=peak, frac_peak=round(achieved / peak, 4),
         bound=bound, intensity_flop_per_byte=inten, ridge_flop_per_byte=ridge, mfma=mfma, hbm=hbm,
-        algorithmic_bytes=ab,
-        min_hbm_bytes=4 * wl.H * wl.L * wl.D * q.element_size(),
+        split_hbm=split_hbm,
+        min_hbm_bytes=nbytes,
     )
     res["hbm_floor_ms"] = round(res["min_hbm_bytes"] / (HBM_GBPS * 1e9) * 1e3, 5)
+    gb, _, _, gmfma, ghbm = roofline(flops_live, nbytes, graph_ms * 1e-3, dt)
+    res["graph"] = dict(ms_per_step=round(graph_ms, 5), live_tflops=gmfma["achieved"], mfma_frac=gmfma["frac"],
+                        hbm_frac=ghbm["frac"],
+                        protocol="10 forwards captured in one HIP graph, replayed back to back (the device's "
+                                 "rate; a forward of a few microseconds is otherwise paced by the host's "
+                                 "launches), median of 3 rounds of >= 50 ms")
     if iso_ms is not None:
         res["isolated"] = dict(ms_median=round(iso_ms, 5),
                                live_tflops=round(flops_live / (iso_ms * 1e-3) / 1e12, 3),
@@ -575,7 +632,8 @@ def brief(r):
                ms_per_step=r["ms_per_step"], kernel_ms=r["kernel_ms"], live_tflops=r["live_tflops"],
                roofline=dict(bound=r["bound"], intensity_flop_per_byte=r["intensity_flop_per_byte"],
                              ridge_flop_per_byte=r["ridge_flop_per_byte"], mfma=r["mfma"], hbm=r["hbm"]),
-               waste=r["waste"], settle_ms=r["settle_ms"])
+               split_hbm=dict(bytes=r["split_hbm"]["bytes"], frac=r["split_hbm"]["frac"]),
+               graph=r["graph"], waste=r["waste"], settle_ms=r["settle_ms"])
     for key in ("parity", "cpu_baseline"):
         if key in r:
             out[key] = r[key]
@@ -585,7 +643,8 @@ def brief(r):
 def log_result(r):
     log(f"[bench]   {r['ms_per_step']:.4f} ms/step  kernel {r['kernel_ms']:.4f} ms  "
         f"{r['kernel_live_tflops']:.1f} live TFLOP/s (mfma {100 * r['mfma']['frac']:.1f}%, "
-        f"hbm {100 * r['hbm']['frac']:.1f}% of algorithmic bytes; {r['bound']}-bound)  waste {r['waste']}")
+        f"hbm {100 * r['hbm']['frac']:.1f}% of algorithmic bytes; {r['bound']}-bound; split bytes at "
+        f"{100 * r['split_hbm']['frac']:.1f}% of HBM)  waste {r['waste']}  graph {r['graph']['ms_per_step']:.4f} ms")
     if r.get("parity"):
         pr = r["parity"]
         log(f"[bench]   parity: max {pr['max_abs']:.2e} mean {pr['mean_abs']:.2e} over {pr['rows']} rows x "
@@ -617,7 +676,7 @@ def log_result(r):
 
 # the other workloads of the default run: (workload, decomposition variant or None)
 CONFIGS = [("window128-L1k", None), ("dilated8-L8k", None), ("dilated8-L8k", "identity"),
-           ("sinkwin-L32k", None), ("prefixlat-L64k", None)]
+           ("bandlat-L16k", "16x16"), ("sinkwin-L32k", None), ("prefixlat-L64k", None), ("bandlat32-L64k", None)]
 
 
 def main():
@@ -631,6 +690,8 @@ def main():
     ap.add_argument("--variant", default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="only the headline workload")
+    ap.add_argument("--forward-only", action="store_true",
+                    help="time only the forward of the workload (no isolated, permute, decode or backward legs)")
     ap.add_argument("--all", action="store_true")
     ap.add_argument("--report", default=None)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -674,7 +735,8 @@ def main():
 
     name = a.workload or workloads.HEADLINE
     log(f"[bench] {name} {a.variant or ''}")
-    r = run(name, a.steps, a.warmup, with_cpu=not a.no_cpu, variant=a.variant, settle_ms=a.settle_ms)
+    r = run(name, a.steps, a.warmup, with_cpu=not a.no_cpu, variant=a.variant, settle_ms=a.settle_ms,
+            extras=not a.forward_only)
     log_result(r)
     configs = []
     if not a.no_configs and a.workload is None:
@@ -701,12 +763,16 @@ def main():
                       traffic_unit="HBM bytes per step (all launches of one step)", traffic_source=traffic_src,
                       intensity_flop_per_byte=r["intensity_flop_per_byte"],
                       ridge_flop_per_byte=r["ridge_flop_per_byte"], mfma=r["mfma"], hbm=r["hbm"],
+                      split_hbm=r["split_hbm"],
                       kernel=" + ".join(sorted({p["kernel"] for p in r["pieces"] if p["kernel"]})) +
                              " (all launches of one step, durations from HIP events on the launch stream"
                              " around each launch of every fourth timed step; a bracket also holds its own"
                              " event record, so the launches' sum can exceed the wall time per step)",
                       algorithmic="live FLOP = 4 * D * live pairs * heads; algorithmic bytes = Q, K, V read "
-                                  "and O, LSE written once per launch, plus the merge input of a second piece"),
+                                  "once and O written once per forward (4 * H * L * D elements); the bound is "
+                                  "the one their ratio selects against the ridge (peak FLOP/s over 8 TB/s). "
+                                  "split_hbm: the bytes the two-pass split as built must move at least"),
+        graph=r["graph"],
         parity=r.get("parity"),
         cpu_baseline=r.get("cpu_baseline"),
         configs=configs,

@@ -145,7 +145,9 @@ int pa_index_steps(const int32_t* kv_idx, const int32_t* kv_num, const int8_t* k
  * (1 if j is the item's first step) | (2 if its last) | (4 for piece 1) | item_qb << 3,
  * word 10 = item_bh and word 11 = item_sync (-1: none).  An item whose list is empty must
  * be given one row: it gets a step with every code 0 (the kernel writes zeros and
- * log-sum-exp -inf for it, or leaves a merged row as it was). */
+ * log-sum-exp -inf for it, or leaves a merged row as it was).  A run row holds rows of
+ * the whole tensor as int32: (max item_bh + 1) * N must stay below 2^31 (not checked here,
+ * the heads are on the device; schedule.py checks it before the call). */
 int pa_index_run(const int32_t* const* steps, const int64_t* steps_pitch, const int32_t* boff_base, int32_t n_pieces,
                  int64_t N, const int32_t* item_piece, const int32_t* item_bh, const int32_t* item_qb,
                  const int32_t* item_sync, const int32_t* item_off, int32_t n_items, int32_t* run, void* stream);

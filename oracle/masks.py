@@ -25,6 +25,7 @@ NAMED = {
     "dilated-32": (((DILATED, 32, 0, 0),), ()),
     "local256+str8": (((LOCAL_STRIDED, 256, 8, 0),), ()),
     "band256+lat16": (((LOCAL_STRIDED, 256, 16, 0),), ()),
+    "band256+lat32": (((LOCAL_STRIDED, 256, 32, 0),), ()),
     "twoband-1024": (((TWOBAND, 128, 1024, 128),), ()),
     "twoband-1000": (((TWOBAND, 128, 1000, 128),), ()),
     "sinks4+win256": (((SINKS, 256, 4, 0),), ()),
@@ -35,6 +36,7 @@ NAMED = {
     "prefixlm-2048": (((PREFIX_LM, 2048, 0, 0),), ()),
     "lat16-band256": (((DILATED, 16, 0, 0),), ((WINDOW, 256, 0, 0),)),
     "lat32-prefixlm2048": (((DILATED, 32, 0, 0),), ((PREFIX_LM, 2048, 0, 0),)),
+    "lat32-band256": (((DILATED, 32, 0, 0),), ((WINDOW, 256, 0, 0),)),
 }
 
 

@@ -44,8 +44,9 @@ constexpr int kRunFirst = 1;
 constexpr int kRunLast = 2;
 constexpr int kRunPiece = 4;
 constexpr int kRunQbShift = 3;
-// polls of a sync counter before a merge gives up (each poll sleeps ~0.4 us); once one
-// merge has given up (*run_status set), the others stop waiting at once
+// polls of a sync counter before a merge gives up (each poll sleeps ~0.4 us); every wait is
+// bounded on its own, so a *run_status left set by an earlier launch (cleared only by the
+// host, with the counters) does not shorten this launch's waits
 constexpr int kRunMaxPolls = 1 << 20;
 
 template <typename T>
@@ -217,7 +218,6 @@ void attn_run_kernel(const AttnK a) {
             __hip_atomic_store(a.run_status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
           }
-          if (__hip_atomic_load(a.run_status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
           __builtin_amdgcn_s_sleep(16);
         }
       }

@@ -74,7 +74,9 @@ __device__ __forceinline__ float dot2_sum<_Float16>(uint32_t packed, float acc) 
 // second-piece item waits for its group's count before it reads those rows to merge them.
 // Work-groups are dispatched in id order and the items a second-piece item waits for have
 // lower ids, so they are running or done when it waits; the wait is also bounded (a merge
-// that gives up sets *run_status).  The last merge of a group zeroes the group's counters.
+// that gives up sets *run_status, which only the host clears, together with the counters;
+// a status left set by an earlier launch does not shorten this launch's waits).  The last
+// merge of a group zeroes the group's counters.
 template <typename T, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_stream_kernel(const AttnK a) {
@@ -370,8 +372,7 @@ void attn_stream_kernel(const AttnK a) {
         int polls_ = 0;                                                                           \
         while (__hip_atomic_load(a.run_sync + sg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <   \
                a.run_sync_signal) {                                                               \
-          if (++polls_ >= kSplitMaxPolls ||                                                       \
-              __hip_atomic_load(a.run_status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) { \
+          if (++polls_ >= kSplitMaxPolls) {                                                       \
             __hip_atomic_store(a.run_status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);      \
             break;                                                                                \
           }                                                                                       \

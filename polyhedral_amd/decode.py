@@ -52,6 +52,8 @@ class DecodeLaunch:
 
 # classes of the largest residue basis a cache may use (the library's limit too)
 MAX_CLASSES = 4096
+# size of the library's per-GPU scratch that pa_decode_fwd_static writes its partials to
+STATIC_SCRATCH_BYTES = 8 << 20
 
 
 class KVCache:
@@ -161,11 +163,16 @@ class KVCache:
             if lse.dtype != torch.float32 or lse.shape != (BH, nq) or lse.stride(1) != 1:
                 raise ValueError("lse must be float32 [BH, nq] with unit stride")
             a.lse, a.lse_sb = _lib.ptr(lse), lse.stride(0)
+        # the split partials' size is known before any state changes: a static call that
+        # would not fit the library's scratch is refused here, not at launch time
+        nbytes = ctypes.c_int64(0)
+        _lib.check(_lib.lib().pa_decode_workspace(ctypes.byref(a), ctypes.byref(nbytes)), "pa_decode_workspace")
         if static_scratch:
+            if nbytes.value > STATIC_SCRATCH_BYTES:
+                raise ValueError(f"the split partials need {nbytes.value} bytes, more than the library's "
+                                 f"{STATIC_SCRATCH_BYTES}-byte scratch (use static_scratch=False)")
             launch = DecodeLaunch(a, [q, o, lse, dm, self.k, self.v] + keep_new, o, dev, static_scratch=True)
         else:
-            nbytes = ctypes.c_int64(0)
-            _lib.check(_lib.lib().pa_decode_workspace(ctypes.byref(a), ctypes.byref(nbytes)), "pa_decode_workspace")
             ws = torch.empty(max(1, (nbytes.value + 3) // 4), dtype=torch.float32, device=dev)
             a.workspace, a.workspace_bytes = _lib.ptr(ws), ws.numel() * 4
             launch = DecodeLaunch(a, [q, o, lse, dm, ws, self.k, self.v] + keep_new, o, dev)
@@ -174,7 +181,13 @@ class KVCache:
 
     def attend(self, q, mask, scale=None, qpos0=None, out=None, lse=None, length=None, static_scratch=False,
                k_new=None, v_new=None):
-        """o [BH, nq, D]: see prepare."""
+        """o [BH, nq, D]: see prepare.  If the launch fails, the cache's length is left as it
+        was (the appended tokens are not counted)."""
+        before = self.length
         launch = self.prepare(q, mask, scale, qpos0, out, lse, length, static_scratch, k_new, v_new)
-        with torch.cuda.device(self.device):
-            return launch()
+        try:
+            with torch.cuda.device(self.device):
+                return launch()
+        except Exception:
+            self.length = before
+            raise

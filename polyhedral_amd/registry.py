@@ -18,6 +18,7 @@ PREFIX_LM = 6
 
 _LAT16_NO_BAND = MaskSpec(((DILATED, 16, 0, 0),), ((WINDOW, 256, 0, 0),))
 _LAT32_NO_PREFIX = MaskSpec(((DILATED, 32, 0, 0),), ((PREFIX_LM, 2048, 0, 0),))
+_LAT32_NO_BAND = MaskSpec(((DILATED, 32, 0, 0),), ((WINDOW, 256, 0, 0),))
 
 SPECS = {
     # the reference's entries (gpu/masks_gpu.py:11-25)
@@ -42,6 +43,9 @@ SPECS = {
     "prefixlm-2048":  (PREFIX_LM, 2048, 0, 0, lambda: masks.PrefixLM(2048)),
     "lat32-prefixlm2048": (_LAT32_NO_PREFIX, 0, 0, 0,
                            lambda: masks.Difference(masks.Dilated(32), masks.PrefixLM(2048))),
+    "band256+lat32":  (LOCAL_STRIDED, 256, 32, 0, lambda: masks.LocalStrided(256, 32)),
+    "lat32-band256":  (_LAT32_NO_BAND, 0, 0, 0,
+                       lambda: masks.Difference(masks.Dilated(32), masks.SlidingWindow(256))),
 }
 
 

@@ -78,6 +78,9 @@ def assign(lengths, BH, groups, keep_empty=True, xcds=XCDS):
 
 def _index_run(pieces_steps, boff_base, N, item_piece, item_bh, item_qb, item_sync, item_len, dev):
     """Run rows (int32 [rows, 16]) of items listed in run order (pa_index_run)."""
+    if item_bh.size and (int(np.max(item_bh)) + 1) * int(N) >= 2 ** 31:
+        raise ValueError(f"run rows hold rows of the whole [BH, N] tensor as int32: {int(np.max(item_bh)) + 1} "
+                         f"heads of N={N} rows do not fit")
     off = np.zeros(item_len.size + 1, dtype=np.int64)
     np.cumsum(item_len, out=off[1:])
     total = int(off[-1])

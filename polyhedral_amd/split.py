@@ -244,18 +244,25 @@ class SplitPlan:
         return (self._runs[key], 0)
 
     def forward(self, q, k, v, scale=None, out=None, lse=None):
-        """o [BH, N, D] in q's dtype; lse (float32 [BH, N]) receives the merged log-sum-exp."""
+        """o [BH, N, D] in q's dtype; lse (float32 [BH, N]) receives the merged log-sum-exp.
+        A split run as one launch (fuse) is checked before returning: if a merge gave up
+        waiting for its rows, the counters are cleared and RuntimeError is raised."""
         launches, o, _ = self.prepare(q, k, v, scale, out, lse)
         with torch.cuda.device(q.device):
             for launch in launches:
                 launch()
+        if any(isinstance(x, SplitLaunch) for x in launches):
+            self.check()
         return o
 
 
 class SplitLaunch:
     """Both pieces of a two-piece split in one persistent launch (pa_attn_fwd_split).
     Calls of one plan over the same tensors must not overlap (they share the sync
-    counters)."""
+    counters).  A merge whose bounded wait gives up marks the schedule's status; check()
+    (a device synchronisation) then raises and clears the status and the counters, which
+    a give-up can leave out of step with the next launch: call it after launches made
+    outside SplitPlan.forward (which checks by itself)."""
 
     kernel = "split"
 
@@ -279,6 +286,10 @@ class SplitLaunch:
     def __call__(self):
         _lib.check(_lib.lib().pa_attn_fwd_split(self._ref, _lib.stream_of(self.out)), "pa_attn_fwd_split")
         return self.out
+
+    def check(self):
+        """Raise if a merge of a past launch gave up waiting; status and counters are cleared."""
+        self.sched.check()
 
 
 def lse_merge(o_parts, lse_parts, out_dtype=torch.float32, lse_out=None):

@@ -13,6 +13,14 @@ reads Q/K/V through the permutation inside the kernel.
                     tiles 128x32, k scaled x4 on the first 64 keys
   prefixlat-L64k    prefix-LM 2048 + (lattice-32 minus prefix-LM) (empty), bf16, H=8,
                     L=65536, D=128, tiles 128x32, one pass per sub-mask
+  bandlat32-L64k    the non-degenerate companion at the prefix-LM workload's shape (H=8,
+                    L=65536, D=128, bf16), whose second sub-mask is not empty, so the
+                    log-sum-exp combine of two passes runs at L = 65536:
+                    0 <= q-kv < 256 or (q-kv) % 32 == 0, split into band-256 (identity,
+                    128x32) + lattice-32 minus band (rp32, 128x32)
+
+bandlat-L16k also has the variant "16x16": the same two pieces on their 16x16-floor
+block indices (the general kernel, one 16-row wave per query block).
 """
 from dataclasses import dataclass, field
 
@@ -65,7 +73,8 @@ def make(name):
         return Workload(name, "band-256 | lattice-16, bf16, H=32, L=16384, D=128: band (identity, 128x32) "
                               "+ lattice-16 minus band (rp16, 128x32), LSE merge",
                         32, L, 128, torch.bfloat16, [Piece(band, 128, 32), Piece(lat, 128, 32, residue=16)],
-                        union, variants={"single-rp16": [Piece(union, 128, 32, residue=16)]})
+                        union, variants={"single-rp16": [Piece(union, 128, 32, residue=16)],
+                                         "16x16": [Piece(band, 16, 16), Piece(lat, 16, 16, residue=16)]})
     if name == "sinkwin-L32k":
         m = M.SinksWindow(64, 1024)
         return Workload(name, "64 sinks + causal window 1024, bf16, H=32, L=32768, D=128, 128x32 tiles",
@@ -78,8 +87,17 @@ def make(name):
                               "128x32 tiles, one pass per sub-mask",
                         8, L, 128, torch.bfloat16, [Piece(p, 128, 32), Piece(sub2, 128, 32, residue=32)],
                         M.Union(p, M.Dilated(32)))
+    if name == "bandlat32-L64k":
+        L = 65536
+        band = M.SlidingWindow(256)
+        lat = M.Difference(M.Dilated(32), band)
+        return Workload(name, "band-256 | lattice-32, bf16, H=8, L=65536, D=128: band (identity, 128x32) "
+                              "+ lattice-32 minus band (rp32, 128x32), LSE merge (the two-pass companion at "
+                              "the prefix-LM workload's shape)",
+                        8, L, 128, torch.bfloat16, [Piece(band, 128, 32), Piece(lat, 128, 32, residue=32)],
+                        M.LocalStrided(256, 32))
     raise KeyError(name)
 
 
-NAMES = ["window128-L1k", "dilated8-L8k", "bandlat-L16k", "sinkwin-L32k", "prefixlat-L64k"]
+NAMES = ["window128-L1k", "dilated8-L8k", "bandlat-L16k", "sinkwin-L32k", "prefixlat-L64k", "bandlat32-L64k"]
 HEADLINE = "bandlat-L16k"

@@ -35,6 +35,7 @@ CASES = [
     ("sinks64+win1024", 32768, 1, 128, 32), ("sinks64+win1024", 32768, 1, 16, 16),
     ("prefixlm-2048", 65536, 1, 128, 32), ("prefixlm-2048", 65536, 1, 16, 16),
     ("lat32-prefixlm2048", 65536, 32, 128, 32), ("lat32-prefixlm2048", 65536, 32, 16, 16),
+    ("window-256", 65536, 1, 128, 32), ("lat32-band256", 65536, 32, 128, 32),
 ]
 
 

@@ -227,3 +227,37 @@ def test_split_grid_headline_equals_per_block(gpu):
     torch.cuda.synchronize()
     grid.check()
     assert torch.equal(o_g, o_b) and torch.equal(lse_g, lse_b)
+
+
+def test_split_grid_give_up_is_reported_and_cleared(gpu):
+    """A merge that never sees its rows published (the launch's sync target raised above
+    the count its group can reach, so every merge exits through its own bounded wait)
+    marks the status: check() raises and clears the status and the counters, and the next
+    launch, with the real target, gives the two-launch result bit for bit (a stale status
+    no longer shortens its waits)."""
+    N, BH = 4096, 2
+    band = pm.SlidingWindow(256)
+    lat = pm.Difference(pm.Dilated(16), band)
+    pieces = [Piece(band, 128, 32), Piece(lat, 128, 32, residue=16)]
+    q, k, v = make_qkv(BH, N, 128, torch.bfloat16, seed=77)
+    qd, kd, vd = (x.to(gpu) for x in (q, k, v))
+    grid = SplitPlan(pieces, N, gpu, fuse=True)
+    blk = SplitPlan(pieces, N, gpu)
+    launches, o_g, lse_g = grid.prepare(qd, kd, vd)
+    (launch,) = launches
+    real = launch.args.sync_signal
+    launch.args.sync_signal = real + 1000      # no group ever reaches it
+    launch()
+    torch.cuda.synchronize()
+    sg = grid._runs[("grid", BH)]
+    assert int(sg.status.item()) == 1
+    with pytest.raises(RuntimeError, match="gave up"):
+        launch.check()
+    assert int(sg.status.item()) == 0 and int(sg.sync.abs().sum()) == 0
+    launch.args.sync_signal = real
+    launch()
+    lse_b = torch.empty(BH, N, device=gpu)
+    o_b = blk.forward(qd, kd, vd, lse=lse_b)
+    torch.cuda.synchronize()
+    launch.check()
+    assert torch.equal(o_g, o_b) and torch.equal(lse_g, lse_b)

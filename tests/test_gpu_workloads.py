@@ -14,7 +14,8 @@ from tests.util import TOL, as64
 pytestmark = pytest.mark.gpu
 
 ORACLE = {"window128-L1k": "window-128", "dilated8-L8k": "dilated-8", "bandlat-L16k": "band256+lat16",
-          "sinkwin-L32k": "sinks64+win1024", "prefixlat-L64k": "prefixlm-2048"}
+          "sinkwin-L32k": "sinks64+win1024", "prefixlat-L64k": "prefixlm-2048",
+          "bandlat32-L64k": "band256+lat32"}
 
 
 def _sample_rows(L, extra=()):
@@ -140,4 +141,48 @@ def test_bandlat_split_equals_single_pass(gpu):
     a = SplitPlan(wl.pieces, wl.L, gpu).forward(q, k, v)
     b = SplitPlan(wl.variants["single-rp16"], wl.L, gpu).forward(q, k, v)
     d = (a.float() - b.float()).abs()
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 2e-3
+
+
+def test_bandlat32_companion_runs_both_passes_and_equals_single_pass(gpu):
+    """The companion at the prefix-LM workload's shape (H=8, L=65536): both sub-masks are
+    non-empty, so the second pass merges into the first by log-sum-exp at L = 65536.
+    Its output equals one pass over the union in the rp32 basis."""
+    wl = workloads.make("bandlat32-L64k")
+    q, k, v = (x.to(gpu) for x in wl.inputs(0, "cpu"))
+    plan = SplitPlan(wl.pieces, wl.L, gpu)
+    assert [b["live"] > 0 for b in plan.built] == [True, True]
+    launches, o, lse = plan.prepare(q, k, v)
+    assert len(launches) == 2 and plan.launched == [(0,), (1,)]
+    for launch in launches:
+        launch()
+    from polyhedral_amd.split import Piece
+    single = SplitPlan([Piece(wl.union, 128, 32, residue=32)], wl.L, gpu).forward(q, k, v)
+    torch.cuda.synchronize()
+    d = (o.float() - single.float()).abs()
+    _log(dict(workload=wl.name, what="split vs single rp32 pass", max_abs=d.max().item(), mean_abs=d.mean().item()))
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 2e-3
+
+
+def test_bandlat_16x16_floor_sampled_rows(gpu):
+    """The headline's two pieces on their 16x16-floor block indices (the general kernel,
+    one 16-row wave per query block) at full size: sampled rows of every head against the
+    float64 oracle, and the same output as the 128x32 split within tolerance."""
+    name = "bandlat-L16k"
+    wl = workloads.make(name)
+    qc, kc, vc = wl.inputs(0, "cpu")
+    q, k, v = (x.to(gpu) for x in (qc, kc, vc))
+    plan = SplitPlan(wl.variants["16x16"], wl.L, gpu)
+    assert [b["tiles"] for b in plan.built] == [17272, 32256]
+    lse = torch.empty(wl.H, wl.L, device=gpu)
+    o = plan.forward(q, k, v, lse=lse)
+    ref = SplitPlan(wl.pieces, wl.L, gpu).forward(q, k, v)
+    torch.cuda.synchronize()
+    rows = _sample_rows(wl.L)
+    heads = list(range(wl.H))
+    mx, mean = _check_rows(name, o.cpu(), lse.cpu(), qc, kc, vc, heads, rows)
+    d = (o.float() - ref.float()).abs()
+    _log(dict(workload=name + "[16x16]", rows=len(rows), heads=len(heads), max_abs=mx, mean_abs=mean,
+              vs_128x32_max=d.max().item()))
+    print(f"{name} 16x16 floor: max abs {mx:.2e} mean abs {mean:.2e}; vs 128x32 split max {d.max().item():.2e}")
     assert d.max().item() <= 2e-2 and d.mean().item() <= 2e-3

@@ -148,3 +148,39 @@ def test_wave_codes_are_consistent_with_the_tile_flags():
                             bit = g * (A // cw) + c
                             assert (code >> (2 * bit)) & 1 == int(sub.any())
                             assert (code >> (2 * bit + 1)) & 1 == int(sub.all())
+
+
+# The band-256 | lattice-32 companion at L = 65536 (the prefix-LM workload's shape with a
+# non-empty second sub-mask), per head, derived in closed form:
+#  * window-256: row i holds min(i + 1, 256) keys, so sum = 256 N - 256 * 255 / 2.  A
+#    128-row block at i0 >= 256 spans columns [i0 - 255, i0 + 127]: 12 tiles of 32, of which
+#    the 4 with columns in [i0 - 128, i0 - 1] are full; block 0 has its 4 diagonal tiles,
+#    block 1 (causal so far) 4 full and 4 diagonal.
+#  * lattice-32 minus band in rp32: class c holds positions 32 t + c, t < 2048, and row t
+#    of a class sees t' <= t - 8 of its own class (32 (t - t') >= 256), so a class is a
+#    2048 x 2048 causal matrix shifted by 8: sum_{t >= 8} (t - 7) = 2040 * 2041 / 2 per
+#    class.  Query block b (t in [128 b, 128 b + 127]) lists key tiles 0 .. 4 b + 3, the
+#    first 4 b - 1 of them full (b >= 1), the last 5 (block 0: 4) partial; max 64 tiles.
+COMPANION = [
+    ("window-256", 65536, 1, dict(live=256 * 65536 - 256 * 255 // 2, tiles=4 + 8 + 510 * 12,
+                                  full=4 + 510 * 4, partial=4 + 4 + 510 * 8, max_kv=12)),
+    ("lat32-band256", 65536, 32, dict(live=32 * 2040 * 2041 // 2, tiles=32 * sum(4 * b + 4 for b in range(16)),
+                                      full=32 * sum(4 * b - 1 for b in range(1, 16)),
+                                      partial=32 * (4 + 15 * 5), max_kv=64)),
+]
+
+
+@pytest.mark.parametrize("name,N,s,want", COMPANION, ids=[c[0] for c in COMPANION])
+def test_companion_counts_closed_form(name, N, s, want):
+    r = _build(name, N, 128, 32, s)
+    assert r["live"] == want["live"]
+    assert int(r["kv_num"].sum()) == want["tiles"] and r["kv_idx"].shape[1] == want["max_kv"]
+    listed = np.concatenate([r["kv_partial"][i, :n] for i, n in enumerate(r["kv_num"])])
+    assert int((listed == 0).sum()) == want["full"] and int((listed == 1).sum()) == want["partial"]
+
+
+def test_companion_union_is_the_disjoint_sum():
+    """band256+lat32 = window-256 + (lattice-32 minus window-256), checked on the oracle's
+    live counts at full size: 83,362,816 live pairs per head."""
+    union = _build("band256+lat32", 65536, 128, 32)["live"]
+    assert union == sum(c[3]["live"] for c in COMPANION) == 83362816

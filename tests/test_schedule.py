@@ -149,3 +149,15 @@ def test_grid_start_order_inverts_the_kernel_mapping():
             x, r = i % XCDS, i // XCDS
             lid = x * per + min(x, rem) + r if r < per else x * per + x + per
             assert hw[lid] == i
+
+
+def test_run_rows_refuse_heads_beyond_int32_rows():
+    """A run row holds rows of the whole [BH, N] tensor as int32; the host refuses a list
+    whose heads would overflow before any device call."""
+    import pytest
+    from polyhedral_amd import schedule as S
+    N = 1 << 20
+    item_bh = np.array([0, 2047], dtype=np.int32)      # 2048 * 2^20 = 2^31
+    with pytest.raises(ValueError, match="int32"):
+        S._index_run([None], [0], N, np.zeros(2), item_bh, np.zeros(2, np.int32), np.full(2, -1),
+                     np.ones(2, np.int64), "cpu")

@@ -66,5 +66,13 @@ def test_static_scratch_rejects_oversized_and_workspace_calls(gpu):
     big = pdec.KVCache(4096, 256, 128, torch.bfloat16, 0, gpu)
     qb = torch.zeros(4096, 8, 128, dtype=torch.bfloat16, device=gpu)
     big.append(qb, qb)
-    with pytest.raises(RuntimeError, match="scratch"):
+    before = big.length
+    with pytest.raises(ValueError, match="scratch"):
         big.attend(qb, numpy_mask("causal"), static_scratch=True)
+    assert big.length == before                # refused before the cache's state changed
+    # the library refuses it too: the same call prepared with a workspace, sent to the
+    # static entry point without one
+    launch = big.prepare(qb, numpy_mask("causal"))
+    launch.args.workspace, launch.args.workspace_bytes = None, 0
+    assert _lib.lib().pa_decode_fwd_static(launch._ref, _lib.stream_of(qb)) == -1
+    assert "scratch" in _lib.lib().pa_last_error().decode()
