@@ -20,14 +20,23 @@ static int raise_lds_limit(K kernel, unsigned long long& configured, const char*
   return PA_OK;
 }
 
-template <typename T, bool SPLIT>
+template <typename T, bool SPLIT, int MODE = 0>
 static int launch_stream_t(const AttnK& a, hipStream_t s, const char* name) {
   static unsigned long long configured = 0ull;
-  if (int rc = raise_lds_limit(&attn_stream_kernel<T, SPLIT>, configured, "hipFuncSetAttribute(attn_stream_kernel)"))
+  if (int rc = raise_lds_limit(&attn_stream_kernel<T, SPLIT, MODE>, configured, "hipFuncSetAttribute(attn_stream_kernel)"))
     return rc;
-  hipLaunchKernelGGL((attn_stream_kernel<T, SPLIT>), dim3((unsigned)a.total_wg), dim3(256), kStreamSmem, s, a);
+  hipLaunchKernelGGL((attn_stream_kernel<T, SPLIT, MODE>), dim3((unsigned)a.total_wg), dim3(256), kStreamSmem, s, a);
   PA_LAUNCH_CHECK(name);
   return PA_OK;
+}
+
+// the mode a launch's arguments allow (0: every option read at run time)
+static int stream_mode(const AttnK& a) {
+  if (a.A != 32) return 0;
+  const bool none = a.residue_s == 0 && !a.gather_q && !a.gather_kv && !a.scatter_o && !a.pred.perm_q && !a.pred.perm_kv;
+  if (none) return 1;
+  if (a.residue_s > 0 && a.gather_q && a.gather_kv && a.scatter_o) return 2;
+  return 0;
 }
 
 template <typename T>
@@ -59,7 +68,14 @@ static int launch_run_t(const AttnK& a, int groups, bool cooperative, hipStream_
 }
 
 int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s) {
-  if (dtype == PA_BF16) return launch_stream_t<__bf16, false>(a, s, "attn_stream_kernel<bf16>");
+  const int mode = stream_mode(a);
+  if (dtype == PA_BF16) {
+    if (mode == 1) return launch_stream_t<__bf16, false, 1>(a, s, "attn_stream_kernel<bf16, index space>");
+    if (mode == 2) return launch_stream_t<__bf16, false, 2>(a, s, "attn_stream_kernel<bf16, residue basis>");
+    return launch_stream_t<__bf16, false>(a, s, "attn_stream_kernel<bf16>");
+  }
+  if (mode == 1) return launch_stream_t<_Float16, false, 1>(a, s, "attn_stream_kernel<f16, index space>");
+  if (mode == 2) return launch_stream_t<_Float16, false, 2>(a, s, "attn_stream_kernel<f16, residue basis>");
   return launch_stream_t<_Float16, false>(a, s, "attn_stream_kernel<f16>");
 }
 

@@ -77,7 +77,10 @@ __device__ __forceinline__ float dot2_sum<_Float16>(uint32_t packed, float acc) 
 // that gives up sets *run_status, which only the host clears, together with the counters;
 // a status left set by an earlier launch does not shorten this launch's waits).  The last
 // merge of a group zeroes the group's counters.
-template <typename T, bool SPLIT>
+// MODE (one work-group per item only): 0 every option from the arguments; 1 index space
+// (no basis, no permutation tables), 32-column tiles; 2 closed-form residue basis with Q and
+// K / V gathered and O scattered through it, 32-column tiles.
+template <typename T, bool SPLIT, int MODE = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_stream_kernel(const AttnK a) {
   constexpr int D = 128;
@@ -123,23 +126,23 @@ void attn_stream_kernel(const AttnK a) {
   // their own query block, so the query rows' loads need not wait for the descriptor.
   const int qb = qb_direct >= 0 ? qb_direct : ((cint*)desc)[13];
   const int n_steps = ((cint*)desc)[14];
-  const int A = a.A;
+  const int A = MODE ? 32 : a.A;
 
   // the piece's basis and role: the launch's arguments, or in a split grid those of the
   // item's piece (the second piece merges into the first piece's output and log-sum-exp)
-  const int res_s = SPLIT ? a.run_res[pc] : a.residue_s;
-  const int res_q = SPLIT ? a.run_qlog2[pc] : a.residue_qlog2;
+  const int res_s = MODE == 1 ? 0 : SPLIT ? a.run_res[pc] : a.residue_s;
+  const int res_q = MODE == 1 ? 0 : SPLIT ? a.run_qlog2[pc] : a.residue_qlog2;
   const int pflags = SPLIT ? a.run_flags[pc] : 0;
-  const bool g_q = SPLIT ? (pflags & kPieceGatherQ) != 0 : a.gather_q != 0;
-  const bool g_kv = SPLIT ? (pflags & kPieceGatherKV) != 0 : a.gather_kv != 0;
-  const bool sc_o = SPLIT ? (pflags & kPieceScatterO) != 0 : a.scatter_o != 0;
+  const bool g_q = MODE ? MODE == 2 : SPLIT ? (pflags & kPieceGatherQ) != 0 : a.gather_q != 0;
+  const bool g_kv = MODE ? MODE == 2 : SPLIT ? (pflags & kPieceGatherKV) != 0 : a.gather_kv != 0;
+  const bool sc_o = MODE ? MODE == 2 : SPLIT ? (pflags & kPieceScatterO) != 0 : a.scatter_o != 0;
   const char* prev_o = (!SPLIT || (pflags & kPieceMerge)) ? a.prev_o : nullptr;
   const bool signal = SPLIT && pc == 0;
   const bool waits = SPLIT && pc == 1;
 
-  const bool closed = res_s != 0;
+  const bool closed = MODE ? MODE == 2 : res_s != 0;
   const int32_t rmask = (1 << res_q) - 1;
-  const bool has_pq = closed || (!SPLIT && a.pred.perm_q);
+  const bool has_pq = MODE ? MODE == 2 : closed || (!SPLIT && a.pred.perm_q);
   const bool gather_kv = g_kv && closed;
   const int rstride = gather_kv ? res_s : 1;
 
