@@ -33,9 +33,13 @@ static int launch_stream_t(const AttnK& a, hipStream_t s, const char* name) {
 // the mode a launch's arguments allow (0: every option read at run time)
 static int stream_mode(const AttnK& a) {
   if (a.A != 32) return 0;
+  // a merge input must be 2-byte (the previous partial in the output's layout) for modes 3, 4
+  const int merge = !a.prev_o ? 0 : a.prev_dtype != PA_F32 ? 2 : -1;
+  if (merge < 0) return 0;
   const bool none = a.residue_s == 0 && !a.gather_q && !a.gather_kv && !a.scatter_o && !a.pred.perm_q && !a.pred.perm_kv;
-  if (none) return 1;
-  if (a.residue_s > 0 && a.gather_q && a.gather_kv && a.scatter_o) return 2;
+  if (none) return 1 + merge;
+  // (a query block of 128 rows then lies inside one class's segment of N / s rows)
+  if (a.residue_s > 0 && a.residue_qlog2 >= 7 && a.gather_q && a.gather_kv && a.scatter_o) return 2 + merge;
   return 0;
 }
 
@@ -70,13 +74,21 @@ static int launch_run_t(const AttnK& a, int groups, bool cooperative, hipStream_
 int launch_attn_stream(const AttnK& a, int dtype, hipStream_t s) {
   const int mode = stream_mode(a);
   if (dtype == PA_BF16) {
-    if (mode == 1) return launch_stream_t<__bf16, false, 1>(a, s, "attn_stream_kernel<bf16, index space>");
-    if (mode == 2) return launch_stream_t<__bf16, false, 2>(a, s, "attn_stream_kernel<bf16, residue basis>");
-    return launch_stream_t<__bf16, false>(a, s, "attn_stream_kernel<bf16>");
+    switch (mode) {
+      case 1: return launch_stream_t<__bf16, false, 1>(a, s, "attn_stream_kernel<bf16, index space>");
+      case 2: return launch_stream_t<__bf16, false, 2>(a, s, "attn_stream_kernel<bf16, residue basis>");
+      case 3: return launch_stream_t<__bf16, false, 3>(a, s, "attn_stream_kernel<bf16, index space, merge>");
+      case 4: return launch_stream_t<__bf16, false, 4>(a, s, "attn_stream_kernel<bf16, residue basis, merge>");
+      default: return launch_stream_t<__bf16, false>(a, s, "attn_stream_kernel<bf16>");
+    }
   }
-  if (mode == 1) return launch_stream_t<_Float16, false, 1>(a, s, "attn_stream_kernel<f16, index space>");
-  if (mode == 2) return launch_stream_t<_Float16, false, 2>(a, s, "attn_stream_kernel<f16, residue basis>");
-  return launch_stream_t<_Float16, false>(a, s, "attn_stream_kernel<f16>");
+  switch (mode) {
+    case 1: return launch_stream_t<_Float16, false, 1>(a, s, "attn_stream_kernel<f16, index space>");
+    case 2: return launch_stream_t<_Float16, false, 2>(a, s, "attn_stream_kernel<f16, residue basis>");
+    case 3: return launch_stream_t<_Float16, false, 3>(a, s, "attn_stream_kernel<f16, index space, merge>");
+    case 4: return launch_stream_t<_Float16, false, 4>(a, s, "attn_stream_kernel<f16, residue basis, merge>");
+    default: return launch_stream_t<_Float16, false>(a, s, "attn_stream_kernel<f16>");
+  }
 }
 
 int launch_attn_split_grid(const AttnK& a, int dtype, hipStream_t s) {

@@ -77,9 +77,12 @@ __device__ __forceinline__ float dot2_sum<_Float16>(uint32_t packed, float acc) 
 // that gives up sets *run_status, which only the host clears, together with the counters;
 // a status left set by an earlier launch does not shorten this launch's waits).  The last
 // merge of a group zeroes the group's counters.
-// MODE (one work-group per item only): 0 every option from the arguments; 1 index space
-// (no basis, no permutation tables), 32-column tiles; 2 closed-form residue basis with Q and
-// K / V gathered and O scattered through it, 32-column tiles.
+// MODE (one work-group per item only): 0 every option from the arguments; the others are
+// compiled for 32-column tiles and one basis, with the merge known: 1 index space (no basis,
+// no permutation tables), 2 closed-form residue basis with Q and K / V gathered and O
+// scattered through it (N / s >= 128, so a query block lies in one class's segment), 3 and
+// 4 the same two merging into a 2-byte previous partial.  The launcher picks the mode from
+// the arguments; every mode gives the same results bit for bit.
 template <typename T, bool SPLIT, int MODE = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_stream_kernel(const AttnK a) {
@@ -126,23 +129,27 @@ void attn_stream_kernel(const AttnK a) {
   // their own query block, so the query rows' loads need not wait for the descriptor.
   const int qb = qb_direct >= 0 ? qb_direct : ((cint*)desc)[13];
   const int n_steps = ((cint*)desc)[14];
+  // the basis of the specialised modes: 1 and 3 index space, 2 and 4 closed-form residue;
+  // 3 and 4 merge into a 2-byte previous partial (its row layout that of the output)
+  constexpr int BASIS = MODE == 0 ? 0 : (MODE == 1 || MODE == 3) ? 1 : 2;
+  constexpr int MERGE = MODE == 0 ? -1 : MODE >= 3 ? 1 : 0;
   const int A = MODE ? 32 : a.A;
 
   // the piece's basis and role: the launch's arguments, or in a split grid those of the
   // item's piece (the second piece merges into the first piece's output and log-sum-exp)
-  const int res_s = MODE == 1 ? 0 : SPLIT ? a.run_res[pc] : a.residue_s;
-  const int res_q = MODE == 1 ? 0 : SPLIT ? a.run_qlog2[pc] : a.residue_qlog2;
+  const int res_s = BASIS == 1 ? 0 : SPLIT ? a.run_res[pc] : a.residue_s;
+  const int res_q = BASIS == 1 ? 0 : SPLIT ? a.run_qlog2[pc] : a.residue_qlog2;
   const int pflags = SPLIT ? a.run_flags[pc] : 0;
-  const bool g_q = MODE ? MODE == 2 : SPLIT ? (pflags & kPieceGatherQ) != 0 : a.gather_q != 0;
-  const bool g_kv = MODE ? MODE == 2 : SPLIT ? (pflags & kPieceGatherKV) != 0 : a.gather_kv != 0;
-  const bool sc_o = MODE ? MODE == 2 : SPLIT ? (pflags & kPieceScatterO) != 0 : a.scatter_o != 0;
-  const char* prev_o = (!SPLIT || (pflags & kPieceMerge)) ? a.prev_o : nullptr;
+  const bool g_q = BASIS ? BASIS == 2 : SPLIT ? (pflags & kPieceGatherQ) != 0 : a.gather_q != 0;
+  const bool g_kv = BASIS ? BASIS == 2 : SPLIT ? (pflags & kPieceGatherKV) != 0 : a.gather_kv != 0;
+  const bool sc_o = BASIS ? BASIS == 2 : SPLIT ? (pflags & kPieceScatterO) != 0 : a.scatter_o != 0;
+  const char* prev_o = MERGE == 0 ? nullptr : (!SPLIT || (pflags & kPieceMerge)) ? a.prev_o : nullptr;
   const bool signal = SPLIT && pc == 0;
   const bool waits = SPLIT && pc == 1;
 
-  const bool closed = MODE ? MODE == 2 : res_s != 0;
+  const bool closed = BASIS ? BASIS == 2 : res_s != 0;
   const int32_t rmask = (1 << res_q) - 1;
-  const bool has_pq = MODE ? MODE == 2 : closed || (!SPLIT && a.pred.perm_q);
+  const bool has_pq = BASIS ? BASIS == 2 : closed || (!SPLIT && a.pred.perm_q);
   const bool gather_kv = g_kv && closed;
   const int rstride = gather_kv ? res_s : 1;
 
@@ -172,7 +179,7 @@ void attn_stream_kernel(const AttnK a) {
   // The previous partial (2-byte types, rows in index order or through the closed-form
   // basis) is DMAed into the K ring at the end of the list: rows 0..63 of the block while
   // the last iteration runs, rows 64..127 at the last step; 16-row segments as for K.
-  const bool prev16 = prev_o && a.prev_dtype != PA_F32;
+  const bool prev16 = MERGE >= 0 ? MERGE == 1 : prev_o && a.prev_dtype != PA_F32;
   const bool prev_dma = prev16 && !(sc_o && has_pq && !closed);
   const bool prev_closed = sc_o && closed;
   const uint32_t p_goff =
@@ -547,17 +554,30 @@ void attn_stream_kernel(const AttnK a) {
       *lo_ = lse_v;
   }
   // (each wave reads back only the rows it wrote: LDS keeps a wave's accesses in order)
+  if constexpr (BASIS != 0) {
+    const int r0 = qb * 128 + w * 32 + (lane >> 4);
+    const int s0 = BASIS == 2 ? (r0 & rmask) * res_s + (r0 >> res_q) : r0;
+    char* dst0 = a.o + (bh * a.o_sb + (int64_t)s0 * a.o_sn) * ESZ + 16 * (lane & 15);
+    const int64_t step_b = (int64_t)4 * (BASIS == 2 ? res_s : 1) * a.o_sn * ESZ;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int rr = 4 * i + (lane >> 4);
-    const u32x4 v = *(lds_u4*)(stage + rr * 256 + 16 * ((lane & 15) ^ (rr & 15)));
-    const int r_ = qb * 128 + w * 32 + rr;
-    const int s_ = (sc_o && has_pq) ? (closed ? (r_ & rmask) * res_s + (r_ >> res_q) : a.pred.perm_q[r_]) : r_;
-    char* dst_ = a.o + (bh * a.o_sb + (int64_t)s_ * a.o_sn) * ESZ + 16 * (lane & 15);
-    if (signal)
-      store_x4_sc1(dst_, v.x, v.y, v.z, v.w);
-    else
-      *reinterpret_cast<u32x4*>(dst_) = v;
+    for (int i = 0; i < 8; ++i) {
+      const int rr = 4 * i + (lane >> 4);
+      const u32x4 v = *(lds_u4*)(stage + rr * 256 + 16 * ((lane & 15) ^ (rr & 15)));
+      *reinterpret_cast<u32x4*>(dst0 + i * step_b) = v;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = 4 * i + (lane >> 4);
+      const u32x4 v = *(lds_u4*)(stage + rr * 256 + 16 * ((lane & 15) ^ (rr & 15)));
+      const int r_ = qb * 128 + w * 32 + rr;
+      const int s_ = (sc_o && has_pq) ? (closed ? (r_ & rmask) * res_s + (r_ >> res_q) : a.pred.perm_q[r_]) : r_;
+      char* dst_ = a.o + (bh * a.o_sb + (int64_t)s_ * a.o_sn) * ESZ + 16 * (lane & 15);
+      if (signal)
+        store_x4_sc1(dst_, v.x, v.y, v.z, v.w);
+      else
+        *reinterpret_cast<u32x4*>(dst_) = v;
+    }
   }
   if constexpr (SPLIT) {
     if (signal) {
