@@ -757,7 +757,7 @@ def main():
                     live_pairs_per_head=r["live_pairs_per_head"], waste=r["waste"],
                     pct_bf16_peak=round(100 * r["live_tflops"] / PEAK_TFLOPS["bf16"], 2),
                     pieces=r["pieces"], index_build_ms=r["index_build_ms"]),
-        settle_ms=r["settle_ms"],
+        settle_ms=r["settle_ms"], settle_forwards=r["settle_forwards"],
         roofline=dict(bound=r["bound"], achieved=main_roof["achieved"], peak=main_roof["peak"],
                       unit=main_roof["unit"], frac=main_roof["frac"], traffic=traffic,
                       traffic_unit="HBM bytes per step (all launches of one step)", traffic_source=traffic_src,
