@@ -2,8 +2,8 @@
 import numpy as np
 import torch
 
-# fp32 1e-5 absolute; bf16 max-abs 2e-2 and mean-abs 2e-3;
-# fp16 the reference gate's 3e-3 (gpu/test_correctness.py:23)
+# tolerances of the path against the float64 oracle: fp32 1e-5 absolute; bf16 max-abs
+# 2e-2 and mean-abs 2e-3; fp16 the reference gate's 3e-3 (gpu/test_correctness.py:23)
 TOL = {torch.float32: (1e-5, None), torch.bfloat16: (2e-2, 2e-3), torch.float16: (3e-3, None)}
 
 TILES_GATE = [(128, 128), (128, 32), (64, 64), (32, 32), (16, 16), (128, 16), (16, 128)]
